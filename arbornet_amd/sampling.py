@@ -1,0 +1,250 @@
+"""Host side of the MI355X sampling step: ctypes binding of libarbor_hip.so and the
+``Sampling`` op that mirrors the managed API a caller of ArborNet would use.
+
+The reference binds its native kernels through P/Invoke declarations
+(ArborNet.Core/Native/PInvoke/CUDA.cs:90-202) and surfaces ops as static methods
+(ArborNet.Core/Functional/Ops.cs:21-393, e.g. ``Ops.Softmax`` at :327). A nonzero native
+status becomes an exception carrying the native message, as ``CUDA.Check`` turns a
+CudaError into InvalidOperationException (CUDA.cs:360-364). This module does the same in
+Python: ``Sampling.sample`` validates nothing itself (the library does), launches on the
+current torch stream, and raises :class:`ArborSamplingError` on any nonzero status.
+
+torch is used only for device buffers and the stream handle; all computation happens in
+the HIP library. There is no CPU fallback: without the built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+from typing import Optional
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = _PKG / "libarbor_hip.so"
+HEADER_PATH = _PKG.parent / "include" / "arbor_sampling.h"
+
+ARBOR_DTYPE_F32 = 0
+ARBOR_DTYPE_BF16 = 1
+ARBOR_FLAG_WRITE_PROBS = 1
+
+ARBOR_ID_EMPTY = -1
+ARBOR_ID_INVALID = -2
+ARBOR_ID_BAD_HISTORY = -3
+
+STATUS_NAMES = {
+    0: "ARBOR_OK",
+    -1: "ARBOR_ERR_NULL",
+    -2: "ARBOR_ERR_STRUCT_SIZE",
+    -3: "ARBOR_ERR_SHAPE",
+    -4: "ARBOR_ERR_DTYPE",
+    -5: "ARBOR_ERR_TEMPERATURE",
+    -6: "ARBOR_ERR_PENALTY",
+    -7: "ARBOR_ERR_TOP_K",
+    -8: "ARBOR_ERR_TOP_P",
+    -9: "ARBOR_ERR_MIN_P",
+    -10: "ARBOR_ERR_HISTORY",
+    -11: "ARBOR_ERR_MASK",
+    -12: "ARBOR_ERR_WORKSPACE",
+    -13: "ARBOR_ERR_FLAGS",
+    -14: "ARBOR_ERR_NO_DEVICE",
+}
+
+
+class ArborSamplingError(RuntimeError):
+    """A nonzero status from libarbor_hip (negative: argument error, positive: HIP error)."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        name = STATUS_NAMES.get(status, f"hipError {status}")
+        super().__init__(f"{name}: {message}")
+
+
+class SamplingParams(ctypes.Structure):
+    """Mirror of ``arbor_sampling_params`` (include/arbor_sampling.h)."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("batch", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("ld_logits", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("temperature", ctypes.c_float),
+        ("repetition_penalty", ctypes.c_float),
+        ("frequency_penalty", ctypes.c_float),
+        ("presence_penalty", ctypes.c_float),
+        ("top_k", ctypes.c_int32),
+        ("top_p", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("hist_len", ctypes.c_int32),
+        ("mask_words", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+    ]
+
+    @classmethod
+    def make(cls, batch: int, vocab: int, **kw) -> "SamplingParams":
+        p = cls()
+        p.struct_size = ctypes.sizeof(cls)
+        p.batch, p.vocab, p.ld_logits = batch, vocab, vocab
+        p.dtype = ARBOR_DTYPE_F32
+        p.temperature, p.repetition_penalty, p.top_p = 1.0, 1.0, 1.0
+        p.mask_words = (vocab + 31) // 32
+        for k, v in kw.items():
+            if not hasattr(p, k):
+                raise AttributeError(k)
+            setattr(p, k, v)
+        return p
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+_lib = None
+
+
+def library() -> ctypes.CDLL:
+    """Load libarbor_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m arbornet_amd.build`")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        vp, sz, i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        P = ctypes.POINTER(SamplingParams)
+        lib.arbor_sample.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+        lib.arbor_sample.restype = i32
+        lib.arbor_sample_workspace_bytes.argtypes = [P]
+        lib.arbor_sample_workspace_bytes.restype = sz
+        lib.arbor_sampling_params_init.argtypes = [P, ctypes.c_int32, ctypes.c_int32]
+        lib.arbor_sampling_params_init.restype = None
+        lib.arbor_device_count.argtypes = [ctypes.POINTER(ctypes.c_int)]
+        lib.arbor_device_count.restype = i32
+        lib.arbor_malloc.argtypes = [ctypes.POINTER(vp), sz]
+        lib.arbor_malloc.restype = i32
+        lib.arbor_free.argtypes = [vp]
+        lib.arbor_free.restype = i32
+        lib.arbor_memcpy.argtypes = [vp, vp, sz, i32]
+        lib.arbor_memcpy.restype = i32
+        lib.arbor_memset.argtypes = [vp, i32, sz]
+        lib.arbor_memset.restype = i32
+        lib.arbor_synchronize.argtypes = []
+        lib.arbor_synchronize.restype = i32
+        lib.arbor_last_error.argtypes = []
+        lib.arbor_last_error.restype = ctypes.c_char_p
+        lib.arbor_abi_version.argtypes = []
+        lib.arbor_abi_version.restype = i32
+        _lib = lib
+    return _lib
+
+
+def header_functions() -> list[str]:
+    """Names of the functions include/arbor_sampling.h declares."""
+    text = HEADER_PATH.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(arbor_[a-z_0-9]+)\s*\(", text, flags=re.M)
+
+
+def check(status: int) -> None:
+    if status != 0:
+        msg = library().arbor_last_error().decode(errors="replace")
+        raise ArborSamplingError(status, msg)
+
+
+def workspace_bytes(params: SamplingParams) -> int:
+    return int(library().arbor_sample_workspace_bytes(ctypes.byref(params)))
+
+
+def sample_raw(params: SamplingParams, logits: int, history: Optional[int], mask: Optional[int],
+               uniforms: int, out_ids: int, out_probs: Optional[int], workspace: int,
+               workspace_bytes_: int, stream: Optional[int]) -> int:
+    """Call arbor_sample with raw device addresses; returns the status (does not raise)."""
+    return int(library().arbor_sample(ctypes.byref(params), logits, history, mask, uniforms, out_ids,
+                                      out_probs, workspace, workspace_bytes_, stream))
+
+
+_workspaces: dict = {}
+
+
+def _workspace(device, nbytes: int):
+    """A zero-filled workspace of at least nbytes on `device`, cached per device. The
+    library leaves a workspace zero-filled after every call, so it is reused as is."""
+    import torch
+
+    key = (device.type, device.index)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+class Sampling:
+    """The sampling op, as the managed ``Sampling`` static class would expose it."""
+
+    @staticmethod
+    def sample(logits, uniforms, *, temperature: float = 1.0, repetition_penalty: float = 1.0,
+               frequency_penalty: float = 0.0, presence_penalty: float = 0.0, top_k: int = 0,
+               top_p: float = 1.0, min_p: float = 0.0, history=None, allow_mask=None,
+               vocab: Optional[int] = None, write_probs: bool = False, out_ids=None, out_probs=None):
+        """Sample one token id per row of ``logits`` ([batch, ld] fp32 or bf16 on a HIP
+        device). ``vocab`` defaults to the row length; ``history`` is [batch, H] int32
+        (-1 = padding), ``allow_mask`` [batch, >= ceil(vocab/32)] int32/uint32 bit words,
+        ``uniforms`` [batch] fp32. Returns int32 ids [batch], or (ids, probs) if
+        ``write_probs``."""
+        import torch
+
+        if logits.dim() != 2:
+            raise ValueError("logits must be [batch, ld]")
+        if logits.stride(1) != 1:
+            raise ValueError("logits rows must be contiguous")
+        dev = logits.device
+        if dev.type != "cuda":
+            raise ArborSamplingError(-14, "logits must live on a HIP device")
+        batch = logits.shape[0]
+        V = int(vocab) if vocab is not None else logits.shape[1]
+        dtype = {torch.float32: ARBOR_DTYPE_F32, torch.bfloat16: ARBOR_DTYPE_BF16}.get(logits.dtype)
+        if dtype is None:
+            raise ArborSamplingError(-4, f"logits dtype {logits.dtype} is not float32 or bfloat16")
+        p = SamplingParams.make(batch, V, ld_logits=logits.stride(0), dtype=dtype, temperature=temperature,
+                                repetition_penalty=repetition_penalty, frequency_penalty=frequency_penalty,
+                                presence_penalty=presence_penalty, top_k=top_k, top_p=top_p, min_p=min_p)
+        hist_ptr = mask_ptr = None
+        if history is not None:
+            history = history.to(device=dev, dtype=torch.int32).contiguous()
+            p.hist_len = history.shape[1]
+            hist_ptr = history.data_ptr()
+        if allow_mask is not None:
+            if allow_mask.dtype not in (torch.int32, torch.uint32):
+                raise ValueError("allow_mask must be int32/uint32 bit words")
+            allow_mask = allow_mask.to(device=dev).contiguous()
+            p.mask_words = allow_mask.shape[1]
+            mask_ptr = allow_mask.data_ptr()
+        uniforms = uniforms.to(device=dev, dtype=torch.float32).contiguous()
+        if uniforms.numel() != batch:
+            raise ValueError("one uniform per row is required")
+        if out_ids is None:
+            out_ids = torch.empty(batch, dtype=torch.int32, device=dev)
+        probs_ptr = None
+        if write_probs:
+            p.flags |= ARBOR_FLAG_WRITE_PROBS
+            if out_probs is None:
+                out_probs = torch.empty((batch, V), dtype=torch.float32, device=dev)
+            probs_ptr = out_probs.data_ptr()
+        need = workspace_bytes(p)
+        if need == 0:  # invalid params: let arbor_sample report why
+            need = 256
+        ws = _workspace(dev, need)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        check(sample_raw(p, logits.data_ptr(), hist_ptr, mask_ptr, uniforms.data_ptr(), out_ids.data_ptr(),
+                         probs_ptr, ws.data_ptr(), ws.numel(), stream))
+        return (out_ids, out_probs) if write_probs else out_ids
+
+
+def params_for(workload, write_probs: bool = False) -> SamplingParams:
+    """SamplingParams of a synthetic.Workload."""
+    return SamplingParams.make(
+        workload.batch, workload.vocab, ld_logits=workload.row_stride,
+        dtype=ARBOR_DTYPE_BF16 if workload.dtype == "bf16" else ARBOR_DTYPE_F32,
+        temperature=workload.temperature, repetition_penalty=workload.repetition_penalty,
+        frequency_penalty=workload.frequency_penalty, presence_penalty=workload.presence_penalty,
+        top_k=workload.top_k, top_p=workload.top_p, min_p=workload.min_p, hist_len=workload.hist_len,
+        mask_words=workload.mask_words, flags=ARBOR_FLAG_WRITE_PROBS if write_probs else 0)

@@ -1,0 +1,211 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X sampling step (one JSON line on stdout).
+
+A step is one arbor_sample call over one batch of synthetic logits already resident in
+HBM. The workload is BASELINE.json's headline configuration (c3: B=256, V=128256 fp32,
+T=0.7, top-k 50 then top-p 0.95, repetition penalty 1.15 over a 1024-token history).
+Input sets are rotated so their total exceeds the 256 MB Infinity Cache plus L2, so each
+call reads its logits from HBM.
+
+value       rows/s over the timed steps (barrier + synchronize on both sides)
+roofline    algorithmic bytes per call / average kernel duration (HIP events around
+            every launch on the launch stream), against 8 TB/s
+cpu_baseline  the C oracle (a scalar restatement of the step) on this host, 1 thread,
+            on a bounded sample of rows of the same workload
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "sampled rows/sec at B=256, V=128256 fp32; achieved HBM GB/s vs roofline"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c3", help="c1..c5 (c3 is the headline)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline budget")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sets", type=int, default=0, help="input sets rotated (0 = auto)")
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def traffic_from_profiles(cfg: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE),
+    committed under profiles/ as JSON; None if not measured."""
+    f = ROOT / "profiles" / f"traffic_{cfg}.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the sampling step does not shard across GPUs in this "
+              f"build); got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from arbornet_amd import sampling as S
+    from arbornet_amd import synthetic as syn
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    S.library()
+    w = syn.CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    inp = syn.generate(w)
+    set_bytes = w.algorithmic_bytes()
+    nsets = args.sets or max(2, int(np.ceil((288 << 20) * 1.5 / set_bytes)))
+    nsets = min(nsets, 16)
+
+    def dev_copy(a):
+        if a is None:
+            return None
+        if a.dtype == np.uint16:
+            return torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)
+        if a.dtype == np.uint32:
+            return torch.from_numpy(a.view(np.int32)).to(dev)
+        return torch.from_numpy(a).to(dev)
+
+    base = [dev_copy(inp.logits), dev_copy(inp.history), dev_copy(inp.mask), dev_copy(inp.uniforms)]
+    sets = [base] + [[None if t is None else t.clone() for t in base] for _ in range(nsets - 1)]
+    p = S.params_for(w)
+    need = S.workspace_bytes(p)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    ids = [torch.empty(w.batch, dtype=torch.int32, device=dev) for _ in range(nsets)]
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+
+    def step(i):
+        x, h, m, u = sets[i % nsets]
+        st = S.sample_raw(p, x.data_ptr(), None if h is None else h.data_ptr(),
+                          None if m is None else m.data_ptr(), u.data_ptr(), ids[i % nsets].data_ptr(),
+                          None, ws.data_ptr(), need, sh)
+        if st != 0:
+            S.check(st)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # timed region: per-launch event pairs on the launch stream, plus the wall clock
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t_all0 = torch.cuda.Event(enable_timing=True)
+    t_all1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_all0.record(stream)
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    t_all1.record(stream)
+    torch.cuda.synchronize()
+    wall1 = time.perf_counter()
+    total_ms = t_all0.elapsed_time(t_all1)
+    per_launch_ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
+    kernel_ms = float(per_launch_ms.mean())
+    ms_per_step = total_ms / args.steps
+    rows_per_s = w.batch / (ms_per_step / 1e3)
+
+    # sanity: ids are token ids or sentinels
+    got = ids[0].cpu().numpy()
+    assert np.all((got >= 0) & (got < w.vocab)), "bench produced out-of-range ids"
+
+    achieved_gbs = set_bytes / (kernel_ms / 1e3) / 1e9
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved_gbs, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+        "traffic": traffic_from_profiles(args.config),
+        "algorithmic_bytes": set_bytes,
+        "kernel_ms_mean": round(kernel_ms, 5),
+        "kernel_ms_median": round(float(np.median(per_launch_ms)), 5),
+    }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle
+
+        # bounded sample: whole batches of the same workload, single thread, ~cpu-seconds
+        rows = 0
+        t0 = time.perf_counter()
+        while True:
+            oracle.sample(p, inp.logits, inp.history, inp.mask, inp.uniforms, threads=1)
+            rows += w.batch
+            if time.perf_counter() - t0 >= args.cpu_seconds:
+                break
+        el = time.perf_counter() - t0
+        cpu = {
+            "value": round(rows / el, 1),
+            "unit": "rows/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{rows} rows ({rows // w.batch} full {args.config} batches) in {el:.1f} s, "
+                      f"1 thread of {os.cpu_count()} ({cpu_model()}), inputs in host memory",
+        }
+
+    out = {
+        "metric": METRIC,
+        "value": round(rows_per_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if w.dtype == "f32" else "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.config}: B={w.batch} V={w.vocab} {w.dtype} T={w.temperature} top_k={w.top_k} "
+                        f"top_p={w.top_p} min_p={w.min_p} rep={w.repetition_penalty} freq={w.frequency_penalty} "
+                        f"pres={w.presence_penalty} H={w.hist_len} mask={w.has_mask}",
+            "batch": w.batch,
+            "vocab": w.vocab,
+            "input_sets_rotated": nsets,
+            "wall_s_timed": round(wall1 - wall0, 4),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,150 @@
+/*
+ * arbor_sampling.h -- C ABI of libarbor_hip.so, the MI355X (gfx950) token-sampling
+ * library for ArborNet.
+ *
+ * One call samples one token id per row of a [batch, vocab] logits matrix:
+ *
+ *   logits -> temperature -> repetition / frequency / presence penalty
+ *          -> optional packed allow-mask -> softmax -> top-k -> top-p -> min-p
+ *          -> inverse-CDF draw against a caller-supplied uniform per row.
+ *
+ * Every pointer argument except `params` and the out-param of the helper calls is a
+ * DEVICE pointer. The caller owns all memory, as with the reference's CUDA DLL, whose
+ * kernels never allocate (ArborNet.Core/Backends/CudaBackend.cs:43-46 allocates,
+ * :437-449 frees). Calls are asynchronous and stream-ordered; stream NULL is the
+ * default stream. The library keeps no global state and takes no locks.
+ *
+ * Status convention: 0 = success, negative = argument error (ARBOR_ERR_*, checked on the
+ * host before anything is launched), positive = HIP runtime error code. The message of
+ * the last failure on the calling thread is returned by arbor_last_error(); the managed
+ * side turns a nonzero status into InvalidOperationException the way
+ * ArborNet.Core/Native/PInvoke/CUDA.cs:360-364 (Check) does for CudaError.
+ *
+ * Per-row outcomes that only the device can see are reported through the id itself
+ * (ARBOR_ID_*): all tokens masked or -inf, a NaN / +inf tempered logit, or a history id
+ * >= vocab. Negative history ids are padding and are skipped, so ragged histories are
+ * passed as a [batch, hist_len] matrix padded with -1.
+ */
+#ifndef ARBOR_SAMPLING_H
+#define ARBOR_SAMPLING_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ARBOR_ABI_VERSION 1
+
+/* dtype of the logits matrix */
+#define ARBOR_DTYPE_F32 0
+#define ARBOR_DTYPE_BF16 1
+
+/* flags */
+#define ARBOR_FLAG_WRITE_PROBS 1u /* write the filtered, renormalised q[batch, vocab] */
+
+/* limits */
+#define ARBOR_VOCAB_MAX 1048575     /* 2^20 - 1: ids fit the 20-bit history-table key */
+#define ARBOR_HISTORY_MAX 4096      /* history entries per row */
+
+/* status codes */
+#define ARBOR_OK 0
+#define ARBOR_ERR_NULL (-1)          /* a required pointer is NULL */
+#define ARBOR_ERR_STRUCT_SIZE (-2)   /* params->struct_size != sizeof(arbor_sampling_params) */
+#define ARBOR_ERR_SHAPE (-3)         /* batch <= 0, vocab <= 0 or > ARBOR_VOCAB_MAX, ld_logits < vocab */
+#define ARBOR_ERR_DTYPE (-4)         /* dtype not ARBOR_DTYPE_* */
+#define ARBOR_ERR_TEMPERATURE (-5)   /* temperature not finite and > 0 */
+#define ARBOR_ERR_PENALTY (-6)       /* repetition penalty not finite and > 0; freq/presence not finite */
+#define ARBOR_ERR_TOP_K (-7)         /* top_k < 0 */
+#define ARBOR_ERR_TOP_P (-8)         /* top_p not in (0, 1] */
+#define ARBOR_ERR_MIN_P (-9)         /* min_p not in [0, 1) */
+#define ARBOR_ERR_HISTORY (-10)      /* hist_len < 0 or > ARBOR_HISTORY_MAX, or history NULL with hist_len > 0 */
+#define ARBOR_ERR_MASK (-11)         /* allow_mask given with mask_words < ceil(vocab / 32) */
+#define ARBOR_ERR_WORKSPACE (-12)    /* workspace NULL or smaller than arbor_sample_workspace_bytes() */
+#define ARBOR_ERR_FLAGS (-13)        /* unknown flag bits, or WRITE_PROBS without out_probs */
+#define ARBOR_ERR_NO_DEVICE (-14)    /* no HIP device is visible */
+
+/* per-row sentinel ids written to out_ids */
+#define ARBOR_ID_EMPTY (-1)          /* no finite tempered logit survives (all masked or -inf) */
+#define ARBOR_ID_INVALID (-2)        /* a tempered, penalised, unmasked logit is NaN or +inf */
+#define ARBOR_ID_BAD_HISTORY (-3)    /* the row's history holds an id >= vocab */
+
+/*
+ * Sampling parameters. A host POD passed by pointer; struct_size must equal
+ * sizeof(arbor_sampling_params) so that later ABI versions can grow it.
+ * A filter is disabled by top_k == 0, top_p == 1 or min_p == 0.
+ */
+typedef struct arbor_sampling_params {
+  uint32_t struct_size;
+  int32_t batch;               /* rows */
+  int32_t vocab;               /* columns sampled per row */
+  int32_t ld_logits;           /* elements between row starts, >= vocab */
+  int32_t dtype;               /* ARBOR_DTYPE_F32 or ARBOR_DTYPE_BF16 */
+  float temperature;           /* z = x * (1/temperature) in fp32 */
+  float repetition_penalty;    /* z > 0 ? z * (1/rp) : z * rp, once per distinct history id */
+  float frequency_penalty;     /* z -= count * fp + presence_penalty, per distinct history id */
+  float presence_penalty;
+  int32_t top_k;
+  float top_p;
+  float min_p;
+  int32_t hist_len;            /* history entries per row (row stride of `history`) */
+  int32_t mask_words;          /* uint32 words per row of `allow_mask` (row stride) */
+  uint32_t flags;              /* ARBOR_FLAG_* */
+} arbor_sampling_params;
+
+/*
+ * Sample one id per row.
+ *   logits      [batch, ld_logits] fp32 or bf16 (device)
+ *   history     [batch, hist_len] int32 (device; may be NULL when hist_len == 0)
+ *   allow_mask  [batch, mask_words] uint32, bit (t & 31) of word t >> 5 set = allowed
+ *               (device; NULL = everything allowed)
+ *   uniforms    [batch] fp32 in [0, 1) (device)
+ *   out_ids     [batch] int32 (device)
+ *   out_probs   [batch, vocab] fp32 (device; required iff flags has WRITE_PROBS)
+ *   workspace   device scratch of at least arbor_sample_workspace_bytes(params) bytes,
+ *               zero-filled before its first use; every call leaves it zero-filled
+ *               again, so a workspace may be reused by calls on one stream.
+ *   stream      hipStream_t, or NULL for the default stream
+ * Replaces, for this path, the CUDA DLL entry points the managed side binds through
+ * ArborNet.Core/Native/PInvoke/CUDA.cs:90-202 (NativeSoftmax :192, NativeArgMax :172,
+ * NativeCumSum :178), which the reference composes into no sampler at all.
+ */
+int arbor_sample(const arbor_sampling_params* params, const void* logits,
+                 const int32_t* history, const uint32_t* allow_mask,
+                 const float* uniforms, int32_t* out_ids, float* out_probs,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace arbor_sample needs for these params (0 if params are invalid).
+ * No reference counterpart: the reference's kernels need no scratch (CudaBackend.cs:43-46). */
+size_t arbor_sample_workspace_bytes(const arbor_sampling_params* params);
+
+/* Fill params with defaults for [batch, vocab] fp32 logits: temperature 1, no penalty,
+ * no filter. No reference counterpart (the reference passes arguments positionally). */
+void arbor_sampling_params_init(arbor_sampling_params* params, int32_t batch, int32_t vocab);
+
+/* Number of visible HIP devices. Replaces hipGetDeviceCount as bound by
+ * ArborNet.Core/Native/PInvoke/ROCm.cs:75-76 and CUDA.cs:80-81 (IsAvailable, CUDA.cs:18-30). */
+int arbor_device_count(int* count);
+
+/* Device allocation / release / copy / sync. Replace cudaMalloc, cudaFree, cudaMemcpy and
+ * cudaDeviceSynchronize as bound by ArborNet.Core/Native/PInvoke/CUDA.cs:62-78 (hipMemcpy at
+ * ROCm.cs:86-87). kind follows cudaMemcpyKind / hipMemcpyKind (0..4, CUDA.cs:47-54). */
+int arbor_malloc(void** ptr, size_t bytes);
+int arbor_free(void* ptr);
+int arbor_memcpy(void* dst, const void* src, size_t bytes, int kind);
+int arbor_memset(void* ptr, int value, size_t bytes);
+int arbor_synchronize(void);
+
+/* Message of the last failed call on this thread ("" if none). Replaces the message text
+ * CUDA.Check builds (CUDA.cs:360-364). */
+const char* arbor_last_error(void);
+
+/* ARBOR_ABI_VERSION of the loaded library. No reference counterpart. */
+int arbor_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ARBOR_SAMPLING_H */
