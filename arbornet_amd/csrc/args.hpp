@@ -1,0 +1,102 @@
+// args.hpp -- launch arguments, workload constants and element loads shared by the
+// sampling kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/arbor_sampling.h"
+#include "device_common.hpp"
+
+namespace arbor {
+
+constexpr int kBlock = 1024;               // threads of every sampling workgroup
+constexpr int kWaves = kBlock / kWave;     // 16
+constexpr int kWaveCap = 512;              // candidates a wave holds in LDS while streaming
+constexpr int kFinalCap = 1024;            // candidates a row is finished from
+constexpr int kChunkSlot = 256;            // candidates one chunk of a split row publishes
+constexpr int kMaxTopK = 64;               // largest top-k of the streaming path
+constexpr int kMaxChunks = 64;             // chunks a row may be split into
+constexpr int kMaxChunkLen = 262144;       // ids per chunk (chunk bitmap <= 32 KB)
+constexpr int kMaxHashBits = 13;           // history table slots <= 8192 (H <= 4096)
+
+struct Args {
+  const void* logits;
+  int64_t ld;
+  int V, B;
+  const int32_t* hist;
+  int H;
+  const uint32_t* mask;
+  int mask_words;
+  const float* uniforms;
+  int32_t* out_ids;
+  float* out_probs;
+  float inv_t;
+  Penalty pen;
+  int top_k;          // 0 = off (k >= V is off)
+  float top_p;        // 1 = off
+  float min_p;        // 0 = off
+  float ln_min_p_lo;  // ln(min_p) minus a safety margin: the min-p candidate band
+  int S, chunk_len;
+  int hash_bits, bitmap_words;
+  int aligned, write_probs;
+  uint32_t* hdr;   // [B*S*2]            count, flags of each chunk list
+  uint64_t* cand;  // [B*S*kChunkSlot]   sorted candidate composites of each chunk
+  float* zbuf;     // [B*V]              row solver's tempered logits
+};
+
+template <int DT>
+struct Elem;
+template <>
+struct Elem<ARBOR_DTYPE_F32> {
+  static constexpr int kVec = 4;
+  static constexpr int kBytes = 4;
+  static constexpr int kUnroll = 8;  // 16-byte loads in flight per lane: 32 elements
+  static __device__ __forceinline__ float one(const void* base, int64_t i) {
+    return static_cast<const float*>(base)[i];
+  }
+  static __device__ __forceinline__ void vec(const void* base, int64_t i, float* x) {
+    const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
+  }
+};
+template <>
+struct Elem<ARBOR_DTYPE_BF16> {
+  static constexpr int kVec = 8;
+  static constexpr int kBytes = 2;
+  static constexpr int kUnroll = 4;  // 16-byte loads in flight per lane: 32 elements
+  static __device__ __forceinline__ float one(const void* base, int64_t i) {
+    return bf16_bits_to_float(static_cast<const uint16_t*>(base)[i]);
+  }
+  static __device__ __forceinline__ void vec(const void* base, int64_t i, float* x) {
+    const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[2 * j] = __uint_as_float(w[j] << 16);
+      x[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+    }
+  }
+};
+
+// VEC elements starting at e0 of a row; positions at or beyond `end` read as -inf.
+template <int DT>
+__device__ __forceinline__ void load_unit(const void* row, int e0, int end, bool aligned, float* x) {
+  constexpr int VEC = Elem<DT>::kVec;
+  if (aligned && e0 + VEC <= end) {
+    Elem<DT>::vec(row, e0, x);
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) x[j] = e0 + j < end ? Elem<DT>::one(row, e0 + j) : -INFINITY;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ const void* row_ptr(const Args& a, int row) {
+  return static_cast<const char*>(a.logits) + (size_t)row * (size_t)a.ld * (size_t)Elem<DT>::kBytes;
+}
+
+}  // namespace arbor

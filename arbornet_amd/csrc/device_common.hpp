@@ -3,6 +3,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <float.h>
 #include <stdint.h>
 
 namespace arbor {
@@ -91,19 +92,20 @@ __device__ __forceinline__ uint32_t hist_slot(uint32_t id, uint32_t bits) {
   return (id * 2654435761u) >> (32u - bits);
 }
 
-__device__ __forceinline__ void hist_insert(uint32_t* tab, uint32_t bits, uint32_t id) {
+// Counts one occurrence of id; returns true for the call that created the entry.
+__device__ __forceinline__ bool hist_insert(uint32_t* tab, uint32_t bits, uint32_t id) {
   const uint32_t mask = (1u << bits) - 1u;
   uint32_t s = hist_slot(id, bits);
   for (;;) {
     uint32_t cur = tab[s];
     if (cur == kEmptySlot) {
       const uint32_t prev = atomicCAS(&tab[s], kEmptySlot, id << 12);
-      if (prev == kEmptySlot) return;
+      if (prev == kEmptySlot) return true;
       cur = prev;
     }
     if ((cur >> 12) == id) {
       atomicAdd(&tab[s], 1u);
-      return;
+      return false;
     }
     s = (s + 1u) & mask;
   }

@@ -165,14 +165,14 @@ _workspaces: dict = {}
 
 
 def _workspace(device, nbytes: int):
-    """A zero-filled workspace of at least nbytes on `device`, cached per device. The
-    library leaves a workspace zero-filled after every call, so it is reused as is."""
+    """A workspace of at least nbytes on `device`, cached per device (calls on one device
+    are ordered on torch's current stream, so they may share it)."""
     import torch
 
     key = (device.type, device.index)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
 

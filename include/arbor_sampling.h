@@ -102,9 +102,9 @@ typedef struct arbor_sampling_params {
  *   uniforms    [batch] fp32 in [0, 1) (device)
  *   out_ids     [batch] int32 (device)
  *   out_probs   [batch, vocab] fp32 (device; required iff flags has WRITE_PROBS)
- *   workspace   device scratch of at least arbor_sample_workspace_bytes(params) bytes,
- *               zero-filled before its first use; every call leaves it zero-filled
- *               again, so a workspace may be reused by calls on one stream.
+ *   workspace   device scratch of at least arbor_sample_workspace_bytes(params) bytes;
+ *               its contents need no initialisation. Calls that share a workspace must
+ *               be ordered (the same stream, or synchronised).
  *   stream      hipStream_t, or NULL for the default stream
  * Replaces, for this path, the CUDA DLL entry points the managed side binds through
  * ArborNet.Core/Native/PInvoke/CUDA.cs:90-202 (NativeSoftmax :192, NativeArgMax :172,

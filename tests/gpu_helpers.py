@@ -46,7 +46,7 @@ def run_gpu(params: S.SamplingParams, inp: syn.Inputs, write_probs: bool = False
         params.flags |= S.ARBOR_FLAG_WRITE_PROBS
     need = S.workspace_bytes(params)
     assert need > 0, S.library().arbor_last_error()
-    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    ws = torch.full((need,), 0xA5, dtype=torch.uint8, device="cuda")  # no initialisation needed
     stream = torch.cuda.current_stream().cuda_stream
     outs = []
     for _ in range(repeat):
@@ -56,9 +56,6 @@ def run_gpu(params: S.SamplingParams, inp: syn.Inputs, write_probs: bool = False
         S.check(st)
         torch.cuda.synchronize()
         outs.append(ids.cpu().numpy().copy())
-    # the workspace must be left zero-filled (arrival counters)
-    counters = ws[: 4 * B].view(torch.int32)
-    assert int(counters.abs().sum().item()) == 0, "arrival counters not reset"
     for o in outs[1:]:
         np.testing.assert_array_equal(o, outs[0], err_msg="GPU result not deterministic across calls")
     return outs[0], (probs.cpu().numpy() if write_probs else None)
