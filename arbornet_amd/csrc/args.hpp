@@ -51,12 +51,14 @@ template <>
 struct Elem<ARBOR_DTYPE_F32> {
   static constexpr int kVec = 4;
   static constexpr int kBytes = 4;
-  static constexpr int kUnroll = 8;  // 16-byte loads in flight per lane: 32 elements
+  static constexpr int kUnroll = 3;  // 16-byte loads per lane per batch (double-buffered)
   static __device__ __forceinline__ float one(const void* base, int64_t i) {
     return static_cast<const float*>(base)[i];
   }
+  // streaming 16-byte load: logits are read once, so the load is marked non-temporal
   static __device__ __forceinline__ void vec(const void* base, int64_t i, float* x) {
-    const float4 v = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(static_cast<const float*>(base) + i));
     x[0] = v.x;
     x[1] = v.y;
     x[2] = v.z;
@@ -67,12 +69,13 @@ template <>
 struct Elem<ARBOR_DTYPE_BF16> {
   static constexpr int kVec = 8;
   static constexpr int kBytes = 2;
-  static constexpr int kUnroll = 4;  // 16-byte loads in flight per lane: 32 elements
+  static constexpr int kUnroll = 2;  // 16-byte loads per lane per batch (double-buffered)
   static __device__ __forceinline__ float one(const void* base, int64_t i) {
     return bf16_bits_to_float(static_cast<const uint16_t*>(base)[i]);
   }
   static __device__ __forceinline__ void vec(const void* base, int64_t i, float* x) {
-    const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    const u4 v = __builtin_nontemporal_load(reinterpret_cast<const u4*>(static_cast<const uint16_t*>(base) + i));
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -92,6 +95,38 @@ __device__ __forceinline__ void load_unit(const void* row, int e0, int end, bool
 #pragma unroll
     for (int j = 0; j < VEC; ++j) x[j] = e0 + j < end ? Elem<DT>::one(row, e0 + j) : -INFINITY;
   }
+}
+
+// Raw 16-byte unit (VEC elements) starting at e0; positions at or beyond `end` hold -inf.
+// Kept raw in registers while in flight and converted by unpack_unit when processed.
+template <int DT>
+__device__ __forceinline__ void load_raw(const void* row, int e0, int end, bool aligned, uint32_t* w) {
+  constexpr int VEC = Elem<DT>::kVec;
+  if (aligned && e0 + VEC <= end) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    const u4 v = __builtin_nontemporal_load(
+        reinterpret_cast<const u4*>(static_cast<const char*>(row) + (size_t)e0 * Elem<DT>::kBytes));
+    w[0] = v.x;
+    w[1] = v.y;
+    w[2] = v.z;
+    w[3] = v.w;
+  } else if (DT == ARBOR_DTYPE_F32) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = e0 + j < end ? static_cast<const uint32_t*>(row)[e0 + j] : 0xFF800000u;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = e0 + 2 * j < end ? static_cast<const uint16_t*>(row)[e0 + 2 * j] : 0xFF80u;
+      const uint32_t hi = e0 + 2 * j + 1 < end ? static_cast<const uint16_t*>(row)[e0 + 2 * j + 1] : 0xFF80u;
+      w[j] = lo | (hi << 16);
+    }
+  }
+}
+template <int DT>
+__device__ __forceinline__ float unpack_unit(const uint32_t* w, int j) {
+  if (DT == ARBOR_DTYPE_F32) return __uint_as_float(w[j]);
+  return __uint_as_float((j & 1) ? (w[j >> 1] & 0xFFFF0000u) : (w[j >> 1] << 16));
 }
 
 template <int DT>

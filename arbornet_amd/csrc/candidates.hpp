@@ -227,6 +227,7 @@ struct FinishShared {
   int po[kMaxChunks > kWaves ? kMaxChunks : kWaves];
   double red[kWaves];
   int ints[4];
+  int next_batch;  // streaming: next batch index to hand out
 };
 
 // Union of the prefixes of nl sorted lists that can still reach the final selection:
@@ -332,7 +333,8 @@ __device__ void history_candidates(const Args& a, int row, Lds& L, FinishShared&
       inv = true;
     } else if (z != -INFINITY) {
       const uint64_t c = composite(z, id);
-      if (!MODE_K || c >= s.t0) {
+      // below the non-history bound the final cut can only be higher: drop it here
+      if (MODE_K ? c >= s.t0 : z >= s.zthr) {
         const int pos = atomicAdd(&s.n_uni, 1);
         if (pos < kFinalCap)
           L.uni[pos] = c;

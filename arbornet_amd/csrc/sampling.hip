@@ -31,6 +31,7 @@
 #include "block_ops.hpp"
 #include "candidates.hpp"
 #include "row_solver.hpp"
+#include "topk_path.hpp"
 
 namespace arbor {
 
@@ -54,7 +55,10 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
   const int c1 = min(a.V, c0 + a.chunk_len);
   const void* xrow = row_ptr<DT>(a, row);
 
-  if (t == 0) s.flags = 0u;
+  if (t == 0) {
+    s.flags = 0u;
+    s.next_batch = 0;
+  }
   if (PEN) {
     for (int i = t; i < a.bitmap_words; i += kBlock) L.bitmap[i] = 0u;
     __syncthreads();
@@ -71,6 +75,7 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
   __syncthreads();
 
   // ---- stream the chunk ----
+  // Double-buffered: the loads of batch i+1 are in flight while batch i is processed.
   uint64_t* buf = L.wbuf + wave * kWaveCap;
   uint32_t* rh = L.whist + wave * 256;
   int wc = 0;
@@ -79,32 +84,37 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
   const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
   const bool aligned = a.aligned != 0;
   const int n_units = (c1 - c0 + VEC - 1) / VEC;
-  for (int ub = wave * kUnroll * kWave; ub < n_units; ub += kWaves * kUnroll * kWave) {
+
+  struct Batch {
     float z[kUnroll][VEC];
-    uint32_t mw[kUnroll], bw[kUnroll];
+    uint32_t mw[kUnroll];
+  };
+  auto load = [&](int ub, Batch& bt) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int e0 = c0 + (ub + u * kWave + lane) * VEC;
-      load_unit<DT>(xrow, e0, c1, aligned, z[u]);
-      if (MASK) mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
-      if (PEN) bw[u] = e0 < c1 ? L.bitmap[(e0 - c0) >> 5] : 0u;
+      load_unit<DT>(xrow, e0, c1, aligned, bt.z[u]);
+      if (MASK) bt.mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
     }
+  };
+  // returns false when the wave's list overflowed (min-p band only)
+  auto process = [&](int ub, Batch& bt) -> bool {
     float lmax = -INFINITY;
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int e0 = c0 + (ub + u * kWave + lane) * VEC;
-      const uint32_t mb = MASK ? mw[u] >> (e0 & 31) : ~0u;
-      const uint32_t pb = PEN ? bw[u] >> ((e0 - c0) & 31) : 0u;
+      const uint32_t mb = MASK ? bt.mw[u] >> (e0 & 31) : ~0u;
+      const uint32_t pb = PEN && e0 < c1 ? L.bitmap[(e0 - c0) >> 5] >> ((e0 - c0) & 31) : 0u;
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
-        float v = z[u][j] * a.inv_t;
+        float v = bt.z[u][j] * a.inv_t;
         if (PEN && ((pb >> j) & 1u)) v = -INFINITY;  // history id: evaluated at the finish
         if (MASK && !((mb >> j) & 1u)) v = -INFINITY;
         const bool iv = is_invalid(v);
         bad |= iv;
         v = iv ? -INFINITY : v;
         lmax = fmaxf(lmax, v);
-        z[u][j] = v;
+        bt.z[u][j] = v;
       }
     }
     // raise the threshold from this batch's lane maxima
@@ -119,9 +129,9 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) c += z[u][j] >= thr ? 1 : 0;
+      for (int j = 0; j < VEC; ++j) c += bt.z[u][j] >= thr ? 1 : 0;
     int cnt = wave_sum(c);
-    if (cnt == 0) continue;
+    if (cnt == 0) return true;
     if (wc + cnt > kWaveCap) {
       if (MODE_K) {
         if (wc > a.top_k) thr = fmaxf(thr, wave_keep_topk<kWaveCap>(buf, wc, a.top_k, rh));
@@ -132,7 +142,7 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) c += z[u][j] >= thr ? 1 : 0;
+        for (int j = 0; j < VEC; ++j) c += bt.z[u][j] >= thr ? 1 : 0;
       cnt = wave_sum(c);
     }
     if (wc + cnt <= kWaveCap) {
@@ -141,43 +151,69 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
         const int e0 = c0 + (ub + u * kWave + lane) * VEC;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-          const bool take = z[u][j] >= thr;
+          const bool take = bt.z[u][j] >= thr;
           const uint64_t bal = __ballot(take);
           if (bal) {
-            if (take) buf[wc + lanes_below(bal)] = composite(z[u][j] + 0.0f, e0 + j);
+            if (take) buf[wc + lanes_below(bal)] = composite(bt.z[u][j] + 0.0f, e0 + j);
             wc += __popcll(bal);
           }
         }
       }
-    } else {
-      // a batch larger than the buffer: append 64 at a time, pruning in between
-#pragma unroll 1
-      for (int q = 0; q < kUnroll * VEC; ++q) {
-        float v = -INFINITY;
-#pragma unroll
-        for (int uu = 0; uu < kUnroll; ++uu)
-#pragma unroll
-          for (int jj = 0; jj < VEC; ++jj)
-            if (uu * VEC + jj == q) v = z[uu][jj];
-        const int id = c0 + (ub + (q / VEC) * kWave + lane) * VEC + (q % VEC);
-        if (!__ballot(v >= thr)) continue;
-        if (wc + kWave > kWaveCap) {
-          if (MODE_K)
-            thr = fmaxf(thr, wave_keep_topk<kWaveCap>(buf, wc, a.top_k, rh));
-          else
-            thr = fmaxf(thr, wave_keep_band<kWaveCap>(buf, wc, a.ln_min_p_lo));
-          if (wc + kWave > kWaveCap) {
-            ovf = true;
-            break;
-          }
-        }
-        const bool take = v >= thr;
-        const uint64_t bal = __ballot(take);
-        if (take) buf[wc + lanes_below(bal)] = composite(v + 0.0f, id);
-        wc += __popcll(bal);
-      }
-      if (ovf) break;
+      return true;
     }
+    // a batch larger than the buffer: append 64 at a time, pruning in between
+#pragma unroll 1
+    for (int q = 0; q < kUnroll * VEC; ++q) {
+      float v = -INFINITY;
+#pragma unroll
+      for (int uu = 0; uu < kUnroll; ++uu)
+#pragma unroll
+        for (int jj = 0; jj < VEC; ++jj)
+          if (uu * VEC + jj == q) v = bt.z[uu][jj];
+      const int id = c0 + (ub + (q / VEC) * kWave + lane) * VEC + (q % VEC);
+      if (!__ballot(v >= thr)) continue;
+      if (wc + kWave > kWaveCap) {
+        if (MODE_K)
+          thr = fmaxf(thr, wave_keep_topk<kWaveCap>(buf, wc, a.top_k, rh));
+        else
+          thr = fmaxf(thr, wave_keep_band<kWaveCap>(buf, wc, a.ln_min_p_lo));
+        if (wc + kWave > kWaveCap) return false;
+      }
+      const bool take = v >= thr;
+      const uint64_t bal = __ballot(take);
+      if (take) buf[wc + lanes_below(bal)] = composite(v + 0.0f, id);
+      wc += __popcll(bal);
+    }
+    return true;
+  };
+
+  // batches are handed out from an LDS counter, so faster waves take more of them
+  constexpr int kBatch = kUnroll * kWave;  // units per batch
+  const int n_batches = (n_units + kBatch - 1) / kBatch;
+  auto grab = [&]() -> int {
+    int b = 0;
+    if (lane == 0) b = atomicAdd(&s.next_batch, 1);
+    return __shfl(b, 0);
+  };
+  Batch ba, bb;
+  int bi = grab();
+  if (bi < n_batches) load(bi * kBatch, ba);
+  while (bi < n_batches) {
+    int bn = grab();
+    if (bn < n_batches) load(bn * kBatch, bb);
+    if (!process(bi * kBatch, ba)) {
+      ovf = true;
+      break;
+    }
+    bi = bn;
+    if (bi >= n_batches) break;
+    bn = grab();
+    if (bn < n_batches) load(bn * kBatch, ba);
+    if (!process(bi * kBatch, bb)) {
+      ovf = true;
+      break;
+    }
+    bi = bn;
   }
   // final wave list: exact top-k (or the band of the wave's best), sorted best first
   if (!ovf) {
@@ -223,6 +259,294 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
       a.hdr[slot * 2 + 0] = (fl & kFlagOverflow) ? 0u : (uint32_t)n;
       a.hdr[slot * 2 + 1] = fl;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Streaming top-k (1 <= k <= 64): register-resident candidate lists, see topk_path.hpp
+// ---------------------------------------------------------------------------------------
+struct TopkShared {
+  int next_batch;
+  uint32_t flags;
+  int cnt[kListSlots];
+};
+
+// Dynamic LDS of topk_kernel: per-wave scratch, list slots, history table, chunk bitmap.
+__host__ __device__ constexpr size_t topk_lds_bytes(int hash_slots, int bitmap_words) {
+  return sizeof(uint64_t) * ((size_t)kWaves * kWave + (size_t)kListSlots * kWave) +
+         sizeof(uint32_t) * ((size_t)hash_slots + (size_t)bitmap_words);
+}
+
+template <int DT, bool PEN, bool MASK, bool INLINE>
+__global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
+  constexpr int VEC = Elem<DT>::kVec;
+  constexpr int U = Elem<DT>::kUnroll;
+  constexpr int NQ = VEC * U;           // elements per lane per batch
+  constexpr int kBatch = U * kWave;     // units per batch
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* scratch_all = reinterpret_cast<uint64_t*>(smem);
+  uint64_t* lists = scratch_all + kWaves * kWave;
+  uint32_t* htab = reinterpret_cast<uint32_t*>(lists + kListSlots * kWave);
+  __shared__ TopkShared s;
+
+  const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
+  const int row = blockIdx.x / a.S, chunk = blockIdx.x % a.S;
+  const int c0 = chunk * a.chunk_len;
+  const int c1 = min(a.V, c0 + a.chunk_len);
+  const void* xrow = row_ptr<DT>(a, row);
+  const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
+  const bool own_hist = PEN && chunk == 0;  // this workgroup evaluates the row's history ids
+  const bool hist_wave = own_hist && wave == kWaves - 1;
+  uint32_t* bitmap = htab + (own_hist ? (1 << a.hash_bits) : 0);
+  uint64_t* scr = scratch_all + wave * kWave;
+  const bool aligned = a.aligned != 0;
+  const int n_units = (c1 - c0 + VEC - 1) / VEC;
+  const int n_batches = (n_units + kBatch - 1) / kBatch;
+  const int k = a.top_k;
+
+  struct Batch {
+    uint32_t w[U][4];  // raw 16-byte units
+    uint32_t mw[U];
+  };
+  auto load = [&](int bi, Batch& bt) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e0 = c0 + (bi * kBatch + u * kWave + lane) * VEC;
+      load_raw<DT>(xrow, e0, c1, aligned, bt.w[u]);
+      if (MASK) bt.mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
+    }
+  };
+
+  // the first batch of every streaming wave is in flight during the setup
+  Batch ba, bb;
+  int bi = hist_wave ? n_batches : wave;
+  if (bi < n_batches) load(bi, ba);
+  int32_t hid[(ARBOR_HISTORY_MAX + kBlock - 1) / kBlock];
+  if (PEN) {
+    const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
+#pragma unroll
+    for (int r = 0; r < (ARBOR_HISTORY_MAX + kBlock - 1) / kBlock; ++r) {
+      const int j = t + r * kBlock;
+      hid[r] = j < a.H ? h[j] : -1;
+    }
+  }
+  if (t == 0) {
+    s.next_batch = own_hist ? kWaves - 1 : kWaves;
+    s.flags = 0u;
+    s.cnt[kListSlots - 1] = 0;
+  }
+  if (PEN) {
+    for (int i = t; i < a.bitmap_words; i += kBlock) bitmap[i] = 0u;
+    if (own_hist)
+      for (int i = t; i < (1 << a.hash_bits); i += kBlock) htab[i] = kEmptySlot;
+  }
+  if (a.write_probs) {
+    float* prow = a.out_probs + (size_t)row * (size_t)a.V;
+    for (int i = c0 + t; i < c1; i += kBlock) prow[i] = 0.0f;
+  }
+  __syncthreads();
+  if (PEN) {
+    bool bad = false;
+#pragma unroll
+    for (int r = 0; r < (ARBOR_HISTORY_MAX + kBlock - 1) / kBlock; ++r) {
+      const int32_t id = hid[r];
+      if (id >= a.V) {
+        bad = true;
+      } else if (id >= 0) {
+        if (id >= c0 && id < c1) atomicOr(&bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
+        if (own_hist) hist_insert(htab, (uint32_t)a.hash_bits, (uint32_t)id);
+      }
+    }
+    if (bad) atomicOr(&s.flags, kFlagBadHistory);
+  }
+  __syncthreads();
+
+  // ---- the row's history ids, penalised, as one more list (one wave) ----
+  if (hist_wave) {
+    uint64_t hbest = 0ull;
+    float hthr = -FLT_MAX;
+    bool inv = false;
+    const int P = 1 << a.hash_bits;
+    constexpr int M = 4;
+    for (int s0 = 0; s0 < P; s0 += kWave * M) {
+      int idq[M];
+      uint32_t cq[M], mq[M];
+      float xq[M], zq[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const int slot = s0 + m * kWave + lane;
+        const uint32_t e = slot < P ? htab[slot] : kEmptySlot;
+        idq[m] = e != kEmptySlot ? (int)(e >> 12) : -1;
+        cq[m] = (e & 4095u) + 1u;
+        xq[m] = idq[m] >= 0 ? Elem<DT>::one(xrow, idq[m]) : 0.0f;
+        mq[m] = (MASK && idq[m] >= 0) ? mrow[idq[m] >> 5] : ~0u;
+      }
+      uint32_t pend = 0u;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float z = -INFINITY;
+        if (idq[m] >= 0) {
+          z = penalize(xq[m] * a.inv_t + 0.0f, cq[m], a.pen);
+          if (!((mq[m] >> (idq[m] & 31)) & 1u)) z = -INFINITY;
+          if (is_invalid(z)) {
+            inv = true;
+            z = -INFINITY;
+          }
+        }
+        zq[m] = z;
+        if (z != -INFINITY && z >= hthr) pend |= 1u << m;
+      }
+      list_absorb<M>(hbest, hthr, k, pend, [&](int q) { return zq[q]; }, [&](int q) { return idq[q]; }, scr);
+    }
+    if (__ballot(inv) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
+    const int n = min(k, list_count(hbest));
+    if (lane < n) lists[(kListSlots - 1) * kWave + lane] = hbest;
+    if (lane == 0) s.cnt[kListSlots - 1] = n;
+  }
+
+  // ---- stream the chunk: batches handed out from an LDS counter, double-buffered ----
+  uint64_t best = 0ull;
+  float thr = -FLT_MAX;  // accept z >= thr
+  bool bad = false;
+  auto grab = [&]() -> int {
+    int b = 0;
+    if (lane == 0) b = atomicAdd(&s.next_batch, 1);
+    return __shfl(b, 0);
+  };
+  auto process = [&](int b, Batch& bt) {
+    const int ub = b * kBatch;
+    // tempered logit of slot q; history ids and masked ids read as -inf (history ids are
+    // in the history list), NaN / +inf are flagged and read as -inf
+    auto zof = [&](int q) -> float {
+      const int u = q / VEC, j = q % VEC;
+      const int e0 = c0 + (ub + u * kWave + lane) * VEC;
+      float v = unpack_unit<DT>(bt.w[u], j) * a.inv_t;
+      if (PEN && e0 < c1 && ((bitmap[(e0 - c0) >> 5] >> (((e0 - c0) & 31) + j)) & 1u)) v = -INFINITY;
+      if (MASK && !((bt.mw[u] >> ((e0 & 31) + j)) & 1u)) v = -INFINITY;
+      return is_invalid(v) ? -INFINITY : v;
+    };
+    if (list_count(best) < k) {
+      // until the list holds k entries: the k-th best lane maximum bounds this batch's k-th
+      float lmax = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) lmax = fmaxf(lmax, zof(q));
+      const uint32_t key = wave_sort64_desc_u32(order_key(lmax));
+      thr = fmaxf(thr, key_value(__shfl(key, k - 1)));
+    }
+    uint32_t pend = 0u;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e0 = c0 + (ub + u * kWave + lane) * VEC;
+      const uint32_t mb = MASK ? bt.mw[u] >> (e0 & 31) : ~0u;
+      const uint32_t pb = PEN && e0 < c1 ? bitmap[(e0 - c0) >> 5] >> ((e0 - c0) & 31) : 0u;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float v = unpack_unit<DT>(bt.w[u], j) * a.inv_t;
+        const bool skip = (PEN && ((pb >> j) & 1u)) || (MASK && !((mb >> j) & 1u));
+        bad |= !skip && is_invalid(v);
+        if (!skip && v >= thr && !is_invalid(v)) pend |= 1u << (u * VEC + j);
+      }
+    }
+    list_absorb<NQ>(best, thr, k, pend, zof,
+                    [&](int q) { return c0 + (ub + (q / VEC) * kWave + lane) * VEC + (q % VEC); }, scr);
+  };
+  if (hist_wave) {
+    bi = grab();
+    if (bi < n_batches) load(bi, ba);
+  }
+  while (bi < n_batches) {
+    int bn = grab();
+    if (bn < n_batches) load(bn, bb);
+    process(bi, ba);
+    bi = bn;
+    if (bi >= n_batches) break;
+    bn = grab();
+    if (bn < n_batches) load(bn, ba);
+    process(bi, bb);
+    bi = bn;
+  }
+  {
+    const int n = min(k, list_count(best));
+    if (lane < n) lists[wave * kWave + lane] = best;
+    if (lane == 0) s.cnt[wave] = n;
+    if (__ballot(bad) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
+  }
+  __syncthreads();
+
+  // ---- tree merge of the lists; the result lands in slot 0 ----
+  for (int m = kListSlots, st = 1; m > 1; st *= 2) {
+    if (wave < m / 2) {
+      const int ia = 2 * wave * st, ib = ia + st;
+      const int na = s.cnt[ia], nb = s.cnt[ib];
+      const uint64_t va = lane < na ? lists[ia * kWave + lane] : 0ull;
+      const uint64_t vb = lane < nb ? lists[ib * kWave + lane] : 0ull;
+      const uint64_t v = list_merge(va, vb);
+      const int n = min(k, na + nb);
+      wave_lds_sync();
+      if (lane < n) lists[ia * kWave + lane] = v;
+      if (lane == 0) s.cnt[ia] = n;
+    }
+    m = (m + 1) / 2;
+    __syncthreads();
+  }
+  if (wave != 0) return;
+  const int n = s.cnt[0];
+  const uint32_t flags = s.flags;
+  const uint64_t v = lane < n ? lists[lane] : 0ull;
+  if (INLINE) {
+    if (flags & kFlagBadHistory) {
+      if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
+    } else if (flags & kFlagInvalid) {
+      if (lane == 0) a.out_ids[row] = ARBOR_ID_INVALID;
+    } else if (n == 0) {
+      if (lane == 0) a.out_ids[row] = ARBOR_ID_EMPTY;
+    } else {
+      finish_list(a, row, v, n);
+    }
+  } else {
+    const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
+    if (lane < n) a.cand[slot * kChunkSlot + lane] = v;
+    if (lane == 0) {
+      a.hdr[slot * 2 + 0] = (uint32_t)n;
+      a.hdr[slot * 2 + 1] = flags;
+    }
+  }
+}
+
+// Finishes top-k rows that were split into chunks: one wave per row merges the chunks'
+// lists and draws.
+__global__ void __launch_bounds__(256) topk_finish_kernel(Args a) {
+  const int lane = lane_id();
+  const int row = blockIdx.x * 4 + (int)threadIdx.x / kWave;
+  if (row >= a.B) return;
+  uint32_t flags = 0u;
+  uint64_t best = 0ull;
+  for (int c0 = 0; c0 < a.S; c0 += 8) {
+    uint64_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = c0 + j;
+      v[j] = 0ull;
+      if (c < a.S) {
+        const size_t slot = (size_t)row * (size_t)a.S + (size_t)c;
+        const int n = (int)a.hdr[slot * 2 + 0];
+        flags |= a.hdr[slot * 2 + 1];
+        if (lane < n) v[j] = a.cand[slot * kChunkSlot + lane];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (c0 + j < a.S) best = list_merge(best, v[j]);
+  }
+  const int n = min(a.top_k, list_count(best));
+  if (flags & kFlagBadHistory) {
+    if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
+  } else if (flags & kFlagInvalid) {
+    if (lane == 0) a.out_ids[row] = ARBOR_ID_INVALID;
+  } else if (n == 0) {
+    if (lane == 0) a.out_ids[row] = ARBOR_ID_EMPTY;
+  } else {
+    finish_list(a, row, best, n);
   }
 }
 
@@ -390,7 +714,8 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.chunk_len = len;
     pl.inline_fin = S == 1;
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
-    pl.lds_stream = arbor::lds_total(pl.bitmap_words);
+    pl.lds_stream = pl.mode_k ? arbor::topk_lds_bytes(p->hist_len > 0 ? (1 << hb) : 0, pl.bitmap_words)
+                              : arbor::lds_total(pl.bitmap_words);
     pl.lds_finish = arbor::lds_total(0);
   }
   pl.lds_solver = sizeof(uint32_t) * (size_t)(1 << hb);
@@ -425,14 +750,31 @@ int launch_stream4(bool inl, dim3 grid, size_t lds, hipStream_t st, const arbor:
   return launch(arbor::stream_kernel<DT, PEN, MASK, MODE_K, false>, grid, block, lds, st, a);
 }
 
+// the LDS-buffer streaming kernel serves the min-p band; top-k goes to topk_kernel
 template <int DT, bool PEN, bool MASK>
 int launch_stream3(bool mode_k, bool inl, dim3 grid, size_t lds, hipStream_t st, const arbor::Args& a) {
-  if (mode_k) return launch_stream4<DT, PEN, MASK, true>(inl, grid, lds, st, a);
+  (void)mode_k;
   return launch_stream4<DT, PEN, MASK, false>(inl, grid, lds, st, a);
+}
+
+template <int DT, bool PEN, bool MASK>
+int launch_topk3(const Plan& pl, hipStream_t st, const arbor::Args& a) {
+  const dim3 grid((unsigned)(a.B * pl.S)), block(arbor::kBlock);
+  int r = pl.inline_fin ? launch(arbor::topk_kernel<DT, PEN, MASK, true>, grid, block, pl.lds_stream, st, a)
+                        : launch(arbor::topk_kernel<DT, PEN, MASK, false>, grid, block, pl.lds_stream, st, a);
+  if (r != ARBOR_OK || pl.inline_fin) return r;
+  return launch(arbor::topk_finish_kernel, dim3((unsigned)((a.B + 3) / 4)), dim3(256), 0, st, a);
+}
+
+template <int DT>
+int launch_topk(const Plan& pl, bool pen, bool mask, hipStream_t st, const arbor::Args& a) {
+  if (pen) return mask ? launch_topk3<DT, true, true>(pl, st, a) : launch_topk3<DT, true, false>(pl, st, a);
+  return mask ? launch_topk3<DT, false, true>(pl, st, a) : launch_topk3<DT, false, false>(pl, st, a);
 }
 
 template <int DT>
 int launch_stream(const Plan& pl, bool pen, bool mask, hipStream_t st, const arbor::Args& a) {
+  if (pl.mode_k) return launch_topk<DT>(pl, pen, mask, st, a);
   const dim3 grid((unsigned)(a.B * pl.S));
   int r;
   if (pen)
