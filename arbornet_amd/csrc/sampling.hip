@@ -263,31 +263,120 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Streaming top-k (1 <= k <= 64): register-resident candidate lists, see topk_path.hpp
+// Streaming top-k (1 <= k <= 64)
+//
+//  A. Threshold: the k-th best of the 1024 lane maxima of every wave's first two batches
+//     is a lower bound T0 of the row's k-th best (the k-th best of a subset never exceeds
+//     the k-th best of the whole); it is found with one 2048-bin histogram over the keys'
+//     observed range, taking the lower edge of the bin that holds the k-th maximum.
+//  B. Stream: everything >= the wave's threshold (T0, raised by an exact wave radix
+//     select if the wave's buffer fills) is appended to a per-wave LDS buffer.
+//  C. Select: the wave buffers and the penalised history ids >= T0 form the union; a block
+//     radix select finds its k-th best; one wave sorts the k survivors and draws (fp64).
 // ---------------------------------------------------------------------------------------
+constexpr int kTopkWaveCap = 256;   // candidates one wave buffers
+constexpr int kUnionCap = 4096;     // candidates the row's selection runs over
+constexpr int kSampleBins = 2048;   // histogram bins of the threshold sample
+
 struct TopkShared {
   int next_batch;
   uint32_t flags;
-  int cnt[kListSlots];
+  int n_union;
+  int n_top;
+  float t0;
+  int dsel;
+  uint32_t above, csel;
+  int cnt[kWaves];
+  int off[kWaves + 1];
+  uint32_t red[kWaves];
+  uint64_t red64[kWaves];
 };
 
-// Dynamic LDS of topk_kernel: per-wave scratch, list slots, history table, chunk bitmap.
-__host__ __device__ constexpr size_t topk_lds_bytes(int hash_slots, int bitmap_words) {
-  return sizeof(uint64_t) * ((size_t)kWaves * kWave + (size_t)kListSlots * kWave) +
-         sizeof(uint32_t) * ((size_t)hash_slots + (size_t)bitmap_words);
+// Dynamic LDS of topk_kernel (bytes): wave buffers | histograms | chunk bitmap |
+// history candidates | history table (later the union).
+struct TopkLds {
+  uint64_t* wb;      // [kWaves * kTopkWaveCap]
+  uint32_t* hist;    // [kWaves * 256] (also the 2048-bin sample histogram; solver scratch)
+  uint32_t* bitmap;  // [bitmap_words]
+  uint64_t* hc;      // [hist_len] penalised history candidates
+  uint32_t* htab;    // [1 << hash_bits], then overlaid by
+  uint64_t* uni;     // [kUnionCap]
+  __host__ __device__ static size_t bytes(int bitmap_words, int hist_len, int hash_slots) {
+    const size_t tail = sizeof(uint32_t) * (size_t)hash_slots > sizeof(uint64_t) * kUnionCap
+                            ? sizeof(uint32_t) * (size_t)hash_slots
+                            : sizeof(uint64_t) * kUnionCap;
+    return sizeof(uint64_t) * kWaves * kTopkWaveCap + sizeof(uint32_t) * kWaves * 256 +
+           (sizeof(uint32_t) * (size_t)bitmap_words + 7) / 8 * 8 + sizeof(uint64_t) * (size_t)hist_len + tail;
+  }
+  __device__ TopkLds(unsigned char* base, int bitmap_words, int hist_len) {
+    wb = reinterpret_cast<uint64_t*>(base);
+    hist = reinterpret_cast<uint32_t*>(wb + kWaves * kTopkWaveCap);
+    bitmap = hist + kWaves * 256;
+    hc = reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(bitmap) +
+                                     ((size_t)bitmap_words * sizeof(uint32_t) + 7) / 8 * 8);
+    htab = reinterpret_cast<uint32_t*>(hc + hist_len);
+    uni = reinterpret_cast<uint64_t*>(htab);
+  }
+};
+
+// Composite T such that exactly min(k, n) of the n distinct composites u[0, n) are >= T:
+// MSB-first radix select, 8-bit digits below the highest bit in which they differ.
+template <int BLOCK>
+__device__ uint64_t block_select_kth(const uint64_t* u, int n, int k, uint32_t* hist, TopkShared& s) {
+  const int t = threadIdx.x;
+  if (n <= k) return 0ull;
+  uint64_t lo = ~0ull, hi = 0ull;
+  for (int i = t; i < n; i += BLOCK) {
+    lo = u[i] < lo ? u[i] : lo;
+    hi = u[i] > hi ? u[i] : hi;
+  }
+  lo = block_reduce_min<BLOCK, uint64_t>(lo, s.red64);
+  hi = block_reduce_max<BLOCK, uint64_t>(hi, s.red64);
+  const int hb = 63 - __clzll(hi ^ lo);
+  int shift = hb >= 7 ? hb - 7 : 0;
+  uint64_t pmask = hb >= 63 ? 0ull : (~0ull << (hb + 1));
+  uint64_t prefix = hi & pmask;
+  uint32_t need = (uint32_t)k;
+  for (;;) {
+    if (t < 256) hist[t] = 0u;
+    __syncthreads();
+    for (int i = t; i < n; i += BLOCK) {
+      const uint64_t c = u[i];
+      if ((c & pmask) == prefix) atomicAdd(&hist[(uint32_t)(c >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    const uint32_t cnt = t < 256 ? hist[255 - t] : 0u;  // descending digits
+    uint32_t tot;
+    const uint32_t ex = block_scan_excl<BLOCK, uint32_t>(cnt, s.red, &tot);
+    if (t < 256 && ex < need && ex + cnt >= need) {
+      s.dsel = 255 - t;
+      s.above = ex;
+      s.csel = cnt;
+    }
+    __syncthreads();
+    const int dsel = s.dsel;
+    const uint32_t above = s.above, csel = s.csel;
+    __syncthreads();
+    need -= above;
+    prefix = (prefix & ~(255ull << shift)) | ((uint64_t)dsel << shift);
+    pmask |= 255ull << shift;
+    if (need == csel || shift == 0) return prefix;
+    shift = shift >= 8 ? shift - 8 : 0;
+  }
 }
 
-template <int DT, bool PEN, bool MASK, bool INLINE>
+template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED>
 __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   constexpr int VEC = Elem<DT>::kVec;
   constexpr int U = Elem<DT>::kUnroll;
-  constexpr int NQ = VEC * U;           // elements per lane per batch
-  constexpr int kBatch = U * kWave;     // units per batch
+  constexpr int NQ = VEC * U;                       // elements per lane per batch
+  constexpr int kBatch = U * kWave;                 // units per batch
+  constexpr int HR = (1 << kMaxHashBits) / kBlock;  // history-table slots per thread
+  constexpr int HIDR = (ARBOR_HISTORY_MAX + kBlock - 1) / kBlock;
   extern __shared__ __align__(16) unsigned char smem[];
-  uint64_t* scratch_all = reinterpret_cast<uint64_t*>(smem);
-  uint64_t* lists = scratch_all + kWaves * kWave;
-  uint32_t* htab = reinterpret_cast<uint32_t*>(lists + kListSlots * kWave);
   __shared__ TopkShared s;
+  const bool own_hist = PEN && (blockIdx.x % a.S) == 0;  // this workgroup evaluates the row's history
+  TopkLds L(smem, PEN ? a.bitmap_words : 0, own_hist ? a.H : 0);
 
   const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
   const int row = blockIdx.x / a.S, chunk = blockIdx.x % a.S;
@@ -295,15 +384,13 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   const int c1 = min(a.V, c0 + a.chunk_len);
   const void* xrow = row_ptr<DT>(a, row);
   const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
-  const bool own_hist = PEN && chunk == 0;  // this workgroup evaluates the row's history ids
-  const bool hist_wave = own_hist && wave == kWaves - 1;
-  uint32_t* bitmap = htab + (own_hist ? (1 << a.hash_bits) : 0);
-  uint64_t* scr = scratch_all + wave * kWave;
-  const bool aligned = a.aligned != 0;
   const int n_units = (c1 - c0 + VEC - 1) / VEC;
   const int n_batches = (n_units + kBatch - 1) / kBatch;
   const int k = a.top_k;
 
+  // Aligned rows: every lane issues exactly one 16-byte load per unit (a unit past the
+  // chunk reloads the chunk's last unit and is ignored), so the compiler can count the
+  // loads in flight and the next batch overlaps the current one.
   struct Batch {
     uint32_t w[U][4];  // raw 16-byte units
     uint32_t mw[U];
@@ -311,34 +398,63 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   auto load = [&](int bi, Batch& bt) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int e0 = c0 + (bi * kBatch + u * kWave + lane) * VEC;
-      load_raw<DT>(xrow, e0, c1, aligned, bt.w[u]);
-      if (MASK) bt.mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
+      const int unit = bi * kBatch + u * kWave + lane;
+      if (ALIGNED) {
+        const int e0 = c0 + (unit < n_units ? unit : n_units - 1) * VEC;
+        typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+        const u4 v = __builtin_nontemporal_load(
+            reinterpret_cast<const u4*>(static_cast<const char*>(xrow) + (size_t)e0 * Elem<DT>::kBytes));
+        bt.w[u][0] = v.x;
+        bt.w[u][1] = v.y;
+        bt.w[u][2] = v.z;
+        bt.w[u][3] = v.w;
+        if (MASK) bt.mw[u] = mrow[e0 >> 5];
+      } else {
+        const int e0 = c0 + unit * VEC;
+        load_raw<DT>(xrow, e0, c1, false, bt.w[u]);
+        if (MASK) bt.mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
+      }
     }
   };
+  // tempered logit of slot q of batch b; history ids (scored separately, penalised),
+  // masked ids and units past the chunk read as -inf; NaN / +inf read as -inf (flagged
+  // by `process`)
+  auto zof = [&](int b, const Batch& bt, int q) -> float {
+    const int u = q / VEC, j = q % VEC;
+    const int unit = b * kBatch + u * kWave + lane;
+    const int e0 = c0 + unit * VEC;
+    if (unit >= n_units) return -INFINITY;
+    float v = unpack_unit<DT>(bt.w[u], j) * a.inv_t;
+    if (PEN && ((L.bitmap[(e0 - c0) >> 5] >> (((e0 - c0) & 31) + j)) & 1u)) v = -INFINITY;
+    if (MASK && !((bt.mw[u] >> ((e0 & 31) + j)) & 1u)) v = -INFINITY;
+    return is_invalid(v) ? -INFINITY : v;
+  };
 
-  // the first batch of every streaming wave is in flight during the setup
+  // two batches per wave are in flight while the workgroup sets up
   Batch ba, bb;
-  int bi = hist_wave ? n_batches : wave;
-  if (bi < n_batches) load(bi, ba);
-  int32_t hid[(ARBOR_HISTORY_MAX + kBlock - 1) / kBlock];
+  int ia = wave, ib = wave + kWaves;
+  load(ia, ba);
+  load(ib, bb);
+
+  int32_t hid[HIDR];
   if (PEN) {
     const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
 #pragma unroll
-    for (int r = 0; r < (ARBOR_HISTORY_MAX + kBlock - 1) / kBlock; ++r) {
+    for (int r = 0; r < HIDR; ++r) {
       const int j = t + r * kBlock;
       hid[r] = j < a.H ? h[j] : -1;
     }
   }
   if (t == 0) {
-    s.next_batch = own_hist ? kWaves - 1 : kWaves;
+    s.next_batch = 2 * kWaves;
     s.flags = 0u;
-    s.cnt[kListSlots - 1] = 0;
+    s.n_union = 0;
+    s.n_top = 0;
   }
   if (PEN) {
-    for (int i = t; i < a.bitmap_words; i += kBlock) bitmap[i] = 0u;
+    for (int i = t; i < a.bitmap_words; i += kBlock) L.bitmap[i] = 0u;
     if (own_hist)
-      for (int i = t; i < (1 << a.hash_bits); i += kBlock) htab[i] = kEmptySlot;
+      for (int i = t; i < (1 << a.hash_bits); i += kBlock) L.htab[i] = kEmptySlot;
   }
   if (a.write_probs) {
     float* prow = a.out_probs + (size_t)row * (size_t)a.V;
@@ -348,151 +464,221 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   if (PEN) {
     bool bad = false;
 #pragma unroll
-    for (int r = 0; r < (ARBOR_HISTORY_MAX + kBlock - 1) / kBlock; ++r) {
+    for (int r = 0; r < HIDR; ++r) {
       const int32_t id = hid[r];
       if (id >= a.V) {
         bad = true;
       } else if (id >= 0) {
-        if (id >= c0 && id < c1) atomicOr(&bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
-        if (own_hist) hist_insert(htab, (uint32_t)a.hash_bits, (uint32_t)id);
+        if (id >= c0 && id < c1) atomicOr(&L.bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
+        if (own_hist) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
       }
     }
     if (bad) atomicOr(&s.flags, kFlagBadHistory);
   }
   __syncthreads();
 
-  // ---- the row's history ids, penalised, as one more list (one wave) ----
-  if (hist_wave) {
-    uint64_t hbest = 0ull;
-    float hthr = -FLT_MAX;
-    bool inv = false;
+  // ---- the row's distinct history ids, penalised, into hc[] (every thread: HR slots) ----
+  bool bad = false;
+  if (own_hist) {
     const int P = 1 << a.hash_bits;
-    constexpr int M = 4;
-    for (int s0 = 0; s0 < P; s0 += kWave * M) {
-      int idq[M];
-      uint32_t cq[M], mq[M];
-      float xq[M], zq[M];
+    int idq[HR];
+    uint32_t cq[HR], mq[HR];
+    float xq[HR];
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const int slot = s0 + m * kWave + lane;
-        const uint32_t e = slot < P ? htab[slot] : kEmptySlot;
-        idq[m] = e != kEmptySlot ? (int)(e >> 12) : -1;
-        cq[m] = (e & 4095u) + 1u;
-        xq[m] = idq[m] >= 0 ? Elem<DT>::one(xrow, idq[m]) : 0.0f;
-        mq[m] = (MASK && idq[m] >= 0) ? mrow[idq[m] >> 5] : ~0u;
-      }
-      uint32_t pend = 0u;
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        float z = -INFINITY;
-        if (idq[m] >= 0) {
-          z = penalize(xq[m] * a.inv_t + 0.0f, cq[m], a.pen);
-          if (!((mq[m] >> (idq[m] & 31)) & 1u)) z = -INFINITY;
-          if (is_invalid(z)) {
-            inv = true;
-            z = -INFINITY;
-          }
-        }
-        zq[m] = z;
-        if (z != -INFINITY && z >= hthr) pend |= 1u << m;
-      }
-      list_absorb<M>(hbest, hthr, k, pend, [&](int q) { return zq[q]; }, [&](int q) { return idq[q]; }, scr);
+    for (int r = 0; r < HR; ++r) {
+      const int slot = t + r * kBlock;
+      const uint32_t e = slot < P ? L.htab[slot] : kEmptySlot;
+      idq[r] = e != kEmptySlot ? (int)(e >> 12) : -1;
+      cq[r] = (e & 4095u) + 1u;
+      xq[r] = idq[r] >= 0 ? Elem<DT>::one(xrow, idq[r]) : 0.0f;
+      mq[r] = (MASK && idq[r] >= 0) ? mrow[idq[r] >> 5] : ~0u;
     }
-    if (__ballot(inv) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
-    const int n = min(k, list_count(hbest));
-    if (lane < n) lists[(kListSlots - 1) * kWave + lane] = hbest;
-    if (lane == 0) s.cnt[kListSlots - 1] = n;
+#pragma unroll
+    for (int r = 0; r < HR; ++r) {
+      if (idq[r] < 0) continue;
+      float z = penalize(xq[r] * a.inv_t + 0.0f, cq[r], a.pen);
+      if (!((mq[r] >> (idq[r] & 31)) & 1u)) z = -INFINITY;
+      if (is_invalid(z)) {
+        bad = true;
+      } else if (z != -INFINITY) {
+        L.hc[atomicAdd(&s.n_top, 1)] = composite(z, idq[r]);  // n_top counts hc[] here
+      }
+    }
   }
 
-  // ---- stream the chunk: batches handed out from an LDS counter, double-buffered ----
-  uint64_t best = 0ull;
-  float thr = -FLT_MAX;  // accept z >= thr
-  bool bad = false;
+  // ---- A. threshold from the lane maxima of the first two batches ----
+  {
+    float lm = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zof(ia, ba, q));
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zof(ib, bb, q));
+    const uint32_t key = order_key(lm);
+    const uint32_t kmin = block_reduce_min<kBlock, uint32_t>(key, s.red);
+    const uint32_t kmax = block_reduce_max<kBlock, uint32_t>(key, s.red);
+    const uint32_t span = kmax - kmin;
+    const int sh = span == 0u ? 0 : max(0, 32 - __clz(span) - 11);
+    for (int i = t; i < kSampleBins; i += kBlock) L.hist[i] = 0u;
+    __syncthreads();
+    atomicAdd(&L.hist[(key - kmin) >> sh], 1u);
+    __syncthreads();
+    // bins in descending order, two per thread
+    const uint32_t h0 = L.hist[kSampleBins - 1 - 2 * t], h1 = L.hist[kSampleBins - 2 - 2 * t];
+    uint32_t tot;
+    const uint32_t ex = block_scan_excl<kBlock, uint32_t>(h0 + h1, s.red, &tot);
+    if (t == 0) s.t0 = -FLT_MAX;
+    __syncthreads();
+    int bsel = -1;
+    if (ex < (uint32_t)k && ex + h0 >= (uint32_t)k)
+      bsel = kSampleBins - 1 - 2 * t;
+    else if (ex + h0 < (uint32_t)k && ex + h0 + h1 >= (uint32_t)k)
+      bsel = kSampleBins - 2 - 2 * t;
+    if (bsel >= 0) {
+      const float tz = key_value(kmin + ((uint32_t)bsel << sh));
+      s.t0 = tz > -FLT_MAX ? tz : -FLT_MAX;
+    }
+    __syncthreads();
+  }
+  const float t0 = s.t0;
+
+  // ---- B. stream: batches from an LDS counter, two in flight per wave ----
+  uint64_t* buf = L.wb + wave * kTopkWaveCap;
+  uint32_t* rh = L.hist + wave * 256;
+  int wc = 0;
+  float thr = t0;  // append z >= thr
+  bool ovf = false;
   auto grab = [&]() -> int {
     int b = 0;
     if (lane == 0) b = atomicAdd(&s.next_batch, 1);
     return __shfl(b, 0);
   };
-  auto process = [&](int b, Batch& bt) {
-    const int ub = b * kBatch;
-    // tempered logit of slot q; history ids and masked ids read as -inf (history ids are
-    // in the history list), NaN / +inf are flagged and read as -inf
-    auto zof = [&](int q) -> float {
-      const int u = q / VEC, j = q % VEC;
-      const int e0 = c0 + (ub + u * kWave + lane) * VEC;
-      float v = unpack_unit<DT>(bt.w[u], j) * a.inv_t;
-      if (PEN && e0 < c1 && ((bitmap[(e0 - c0) >> 5] >> (((e0 - c0) & 31) + j)) & 1u)) v = -INFINITY;
-      if (MASK && !((bt.mw[u] >> ((e0 & 31) + j)) & 1u)) v = -INFINITY;
-      return is_invalid(v) ? -INFINITY : v;
-    };
-    if (list_count(best) < k) {
-      // until the list holds k entries: the k-th best lane maximum bounds this batch's k-th
-      float lmax = -INFINITY;
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) lmax = fmaxf(lmax, zof(q));
-      const uint32_t key = wave_sort64_desc_u32(order_key(lmax));
-      thr = fmaxf(thr, key_value(__shfl(key, k - 1)));
-    }
+  __syncthreads();  // the sample histogram is no longer read: wave radix histograms may reuse it
+  auto process = [&](int b, const Batch& bt) {
     uint32_t pend = 0u;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int e0 = c0 + (ub + u * kWave + lane) * VEC;
+      const int unit = b * kBatch + u * kWave + lane;
+      const int e0 = c0 + unit * VEC;
+      const bool valid = unit < n_units;
       const uint32_t mb = MASK ? bt.mw[u] >> (e0 & 31) : ~0u;
-      const uint32_t pb = PEN && e0 < c1 ? bitmap[(e0 - c0) >> 5] >> ((e0 - c0) & 31) : 0u;
+      const uint32_t pb = PEN && valid ? L.bitmap[(e0 - c0) >> 5] >> ((e0 - c0) & 31) : 0u;
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         const float v = unpack_unit<DT>(bt.w[u], j) * a.inv_t;
-        const bool skip = (PEN && ((pb >> j) & 1u)) || (MASK && !((mb >> j) & 1u));
+        const bool skip = !valid || (PEN && ((pb >> j) & 1u)) || (MASK && !((mb >> j) & 1u));
         bad |= !skip && is_invalid(v);
         if (!skip && v >= thr && !is_invalid(v)) pend |= 1u << (u * VEC + j);
       }
     }
-    list_absorb<NQ>(best, thr, k, pend, zof,
-                    [&](int q) { return c0 + (ub + (q / VEC) * kWave + lane) * VEC + (q % VEC); }, scr);
+    if (!__ballot(pend != 0u) || ovf) return;
+    int cnt = wave_sum((int)__popc(pend));
+    if (wc + cnt > kTopkWaveCap) {
+      if (wc > k) thr = fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh));
+#pragma unroll
+      for (int q = 0; q < NQ; ++q)
+        if (((pend >> q) & 1u) && !(zof(b, bt, q) >= thr)) pend &= ~(1u << q);
+      cnt = wave_sum((int)__popc(pend));
+      if (wc + cnt > kTopkWaveCap) {
+        // a batch denser than the buffer: 64 candidates at a time, an exact prune between
+#pragma unroll 1
+        for (int q = 0; q < NQ; ++q) {
+          float v = -INFINITY;
+#pragma unroll
+          for (int qq = 0; qq < NQ; ++qq)
+            if (qq == q && ((pend >> qq) & 1u)) v = zof(b, bt, qq);
+          if (!__ballot(v >= thr)) continue;
+          if (wc + kWave > kTopkWaveCap) {
+            thr = fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh));
+            if (wc + kWave > kTopkWaveCap) {
+              ovf = true;  // unreachable for k <= 64: the row would go to the row solver
+              return;
+            }
+          }
+          const bool take = v >= thr;
+          const uint64_t bal = __ballot(take);
+          if (take) buf[wc + lanes_below(bal)] =
+              composite(v + 0.0f, c0 + (b * kBatch + (q / VEC) * kWave + lane) * VEC + (q % VEC));
+          wc += __popcll(bal);
+        }
+        return;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const bool tk = (pend >> q) & 1u;
+      const uint64_t bal = __ballot(tk);
+      if (bal) {
+        if (tk)
+          buf[wc + lanes_below(bal)] =
+              composite(zof(b, bt, q) + 0.0f, c0 + (b * kBatch + (q / VEC) * kWave + lane) * VEC + (q % VEC));
+        wc += __popcll(bal);
+      }
+    }
   };
-  if (hist_wave) {
-    bi = grab();
-    if (bi < n_batches) load(bi, ba);
+  for (;;) {
+    if (ia >= n_batches) break;
+    process(ia, ba);
+    ia = grab();
+    load(ia, ba);
+    if (ib >= n_batches) break;
+    process(ib, bb);
+    ib = grab();
+    load(ib, bb);
   }
-  while (bi < n_batches) {
-    int bn = grab();
-    if (bn < n_batches) load(bn, bb);
-    process(bi, ba);
-    bi = bn;
-    if (bi >= n_batches) break;
-    bn = grab();
-    if (bn < n_batches) load(bn, ba);
-    process(bi, bb);
-    bi = bn;
-  }
-  {
-    const int n = min(k, list_count(best));
-    if (lane < n) lists[wave * kWave + lane] = best;
-    if (lane == 0) s.cnt[wave] = n;
-    if (__ballot(bad) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
-  }
+  if (lane == 0) s.cnt[wave] = wc;
+  if (__ballot(bad) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
+  if (__ballot(ovf) && lane == 0) atomicOr(&s.flags, kFlagOverflow);
   __syncthreads();
 
-  // ---- tree merge of the lists; the result lands in slot 0 ----
-  for (int m = kListSlots, st = 1; m > 1; st *= 2) {
-    if (wave < m / 2) {
-      const int ia = 2 * wave * st, ib = ia + st;
-      const int na = s.cnt[ia], nb = s.cnt[ib];
-      const uint64_t va = lane < na ? lists[ia * kWave + lane] : 0ull;
-      const uint64_t vb = lane < nb ? lists[ib * kWave + lane] : 0ull;
-      const uint64_t v = list_merge(va, vb);
-      const int n = min(k, na + nb);
-      wave_lds_sync();
-      if (lane < n) lists[ia * kWave + lane] = v;
-      if (lane == 0) s.cnt[ia] = n;
+  // ---- C. union of the wave buffers and the history candidates >= t0; exact top-k ----
+  if (t == 0) {
+    int o = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      s.off[w] = o;
+      o += s.cnt[w];
     }
-    m = (m + 1) / 2;
-    __syncthreads();
+    s.off[kWaves] = o;
+    if (o > kUnionCap) s.flags |= kFlagOverflow;
+    s.n_union = o > kUnionCap ? 0 : o;
   }
-  if (wave != 0) return;
-  const int n = s.cnt[0];
+  __syncthreads();
+  const int n_hc = own_hist ? s.n_top : 0;
+  if (!(s.flags & kFlagOverflow)) {
+    for (int i = lane; i < s.cnt[wave]; i += kWave) L.uni[s.off[wave] + i] = buf[i];
+    for (int i = t; i < n_hc; i += kBlock) {
+      const uint64_t c = L.hc[i];
+      if (composite_z(c) >= t0) {
+        const int pos = atomicAdd(&s.n_union, 1);
+        if (pos < kUnionCap)
+          L.uni[pos] = c;
+        else
+          atomicOr(&s.flags, kFlagOverflow);
+      }
+    }
+  }
+  __syncthreads();
   const uint32_t flags = s.flags;
-  const uint64_t v = lane < n ? lists[lane] : 0ull;
+  if ((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid))) {
+    if (INLINE) {
+      solve_row<kBlock, DT>(a, row, L.htab, *reinterpret_cast<SolverShared*>(L.hist));
+    } else if (t == 0) {
+      const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
+      a.hdr[slot * 2 + 0] = 0u;
+      a.hdr[slot * 2 + 1] = flags;
+    }
+    return;
+  }
+  const int nu = s.n_union;
+  const uint64_t T = block_select_kth<kBlock>(L.uni, nu, k, L.hist, s);
+  if (t == 0) s.n_top = 0;
+  __syncthreads();
+  for (int i = t; i < nu; i += kBlock)
+    if (L.uni[i] >= T) L.wb[atomicAdd(&s.n_top, 1)] = L.uni[i];  // the k best, unordered
+  __syncthreads();
+  if (wave != 0) return;
+  const int n = s.n_top;
+  uint64_t v = lane < n ? L.wb[lane] : 0ull;
+  v = wave_sort64_desc(v);
   if (INLINE) {
     if (flags & kFlagBadHistory) {
       if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
@@ -513,30 +699,42 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   }
 }
 
-// Finishes top-k rows that were split into chunks: one wave per row merges the chunks'
-// lists and draws.
-__global__ void __launch_bounds__(256) topk_finish_kernel(Args a) {
-  const int lane = lane_id();
-  const int row = blockIdx.x * 4 + (int)threadIdx.x / kWave;
-  if (row >= a.B) return;
-  uint32_t flags = 0u;
+// Finishes top-k rows that were split into chunks: wave 0 of a workgroup per row merges
+// the chunks' lists and draws; a row with an overflowed chunk is solved exactly.
+template <int DT>
+__global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ SolverShared ssh;
+  __shared__ uint32_t s_flags;
+  const int lane = lane_id(), row = blockIdx.x;
+  if (threadIdx.x == 0) {
+    uint32_t f = 0u;
+    for (int c = 0; c < a.S; ++c) f |= a.hdr[((size_t)row * (size_t)a.S + (size_t)c) * 2 + 1];
+    s_flags = f;
+  }
+  __syncthreads();
+  const uint32_t flags = s_flags;
+  if ((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid))) {
+    solve_row<kBlock, DT>(a, row, reinterpret_cast<uint32_t*>(smem), ssh);
+    return;
+  }
+  if (threadIdx.x >= kWave) return;
   uint64_t best = 0ull;
-  for (int c0 = 0; c0 < a.S; c0 += 8) {
+  for (int cb = 0; cb < a.S; cb += 8) {
     uint64_t v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int c = c0 + j;
+      const int c = cb + j;
       v[j] = 0ull;
       if (c < a.S) {
         const size_t slot = (size_t)row * (size_t)a.S + (size_t)c;
         const int n = (int)a.hdr[slot * 2 + 0];
-        flags |= a.hdr[slot * 2 + 1];
         if (lane < n) v[j] = a.cand[slot * kChunkSlot + lane];
       }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (c0 + j < a.S) best = list_merge(best, v[j]);
+      if (cb + j < a.S) best = list_merge(best, v[j]);
   }
   const int n = min(a.top_k, list_count(best));
   if (flags & kFlagBadHistory) {
@@ -714,7 +912,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.chunk_len = len;
     pl.inline_fin = S == 1;
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
-    pl.lds_stream = pl.mode_k ? arbor::topk_lds_bytes(p->hist_len > 0 ? (1 << hb) : 0, pl.bitmap_words)
+    pl.lds_stream = pl.mode_k ? arbor::TopkLds::bytes(pl.bitmap_words, p->hist_len, p->hist_len > 0 ? (1 << hb) : 0)
                               : arbor::lds_total(pl.bitmap_words);
     pl.lds_finish = arbor::lds_total(0);
   }
@@ -757,13 +955,21 @@ int launch_stream3(bool mode_k, bool inl, dim3 grid, size_t lds, hipStream_t st,
   return launch_stream4<DT, PEN, MASK, false>(inl, grid, lds, st, a);
 }
 
+template <int DT, bool PEN, bool MASK, bool ALIGNED>
+int launch_topk4(const Plan& pl, hipStream_t st, const arbor::Args& a) {
+  const dim3 grid((unsigned)(a.B * pl.S)), block(arbor::kBlock);
+  int r = pl.inline_fin
+              ? launch(arbor::topk_kernel<DT, PEN, MASK, true, ALIGNED>, grid, block, pl.lds_stream, st, a)
+              : launch(arbor::topk_kernel<DT, PEN, MASK, false, ALIGNED>, grid, block, pl.lds_stream, st, a);
+  if (r != ARBOR_OK || pl.inline_fin) return r;
+  return launch(arbor::topk_finish_kernel<DT>, dim3((unsigned)a.B), block, pl.lds_solver, st, a);
+}
+
 template <int DT, bool PEN, bool MASK>
 int launch_topk3(const Plan& pl, hipStream_t st, const arbor::Args& a) {
-  const dim3 grid((unsigned)(a.B * pl.S)), block(arbor::kBlock);
-  int r = pl.inline_fin ? launch(arbor::topk_kernel<DT, PEN, MASK, true>, grid, block, pl.lds_stream, st, a)
-                        : launch(arbor::topk_kernel<DT, PEN, MASK, false>, grid, block, pl.lds_stream, st, a);
-  if (r != ARBOR_OK || pl.inline_fin) return r;
-  return launch(arbor::topk_finish_kernel, dim3((unsigned)((a.B + 3) / 4)), dim3(256), 0, st, a);
+  // whole 16-byte units only: aligned rows whose length is a multiple of the unit
+  if (a.aligned && a.V % arbor::Elem<DT>::kVec == 0) return launch_topk4<DT, PEN, MASK, true>(pl, st, a);
+  return launch_topk4<DT, PEN, MASK, false>(pl, st, a);
 }
 
 template <int DT>

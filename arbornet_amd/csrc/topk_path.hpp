@@ -15,7 +15,7 @@
 
 namespace arbor {
 
-constexpr int kListSlots = kWaves + 1;  // the waves' lists plus the history list
+constexpr int kListSlots = kWaves;  // one list per wave
 
 // Top-64 of two descending lists (lane i holds the i-th entry), descending.
 __device__ __forceinline__ uint64_t list_merge(uint64_t a, uint64_t b) {
@@ -37,42 +37,48 @@ __device__ __forceinline__ int list_count(uint64_t v) { return __popcll(__ballot
 // z of entry k-1 of a list with at least k entries
 __device__ __forceinline__ float list_kth_z(uint64_t v, int k) { return composite_z(__shfl(v, k - 1)); }
 
-// Collect the lanes' pending candidates (bit q of `pend`: slot q, z = zof(q), id = idof(q))
-// into the wave's list, 64 at a time; once the list holds k entries `thr` rises to its
-// k-th z and pending slots below it are dropped. Wave-uniform control flow. scratch: 64
-// LDS entries private to this wave.
-template <int NQ, typename ZOf, typename IdOf>
-__device__ __forceinline__ void list_absorb(uint64_t& best, float& thr, int k, uint32_t pend, ZOf zof, IdOf idof,
-                                            uint64_t* scratch) {
+// The list shifted down by one lane (lane i gets lane i-1; DPP wave_shr:1, no LDS).
+__device__ __forceinline__ uint64_t list_shift_down(uint64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x138, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x138, 0xF, 0xF, false);
+  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// Insert composite c (wave-uniform) into a descending list, dropping the 64th entry.
+__device__ __forceinline__ uint64_t list_insert(uint64_t best, uint64_t c) {
   const int lane = lane_id();
-  while (__ballot(pend != 0u)) {
-    int base = 0;
+  const int pos = __popcll(__ballot(best > c));
+  const uint64_t down = list_shift_down(best);
+  return lane < pos ? best : (lane == pos ? c : down);
+}
+
+// Insert the lanes' pending candidates (bit q of `pend`: slot q, z = zof(q), id = idof(q))
+// into the wave's list one at a time, skipping those that no longer reach the k-th entry
+// once the list holds k. `thr` tracks the k-th z. Wave-uniform control flow.
+template <int NQ, typename ZOf, typename IdOf>
+__device__ __forceinline__ void list_absorb(uint64_t& best, float& thr, int k, uint32_t pend, ZOf zof, IdOf idof) {
+  uint64_t kth = list_count(best) >= k ? __shfl(best, k - 1) : 0ull;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const bool tk = (pend >> q) & 1u;
-      const uint64_t bal = __ballot(tk);
-      if (bal) {
-        const int pos = base + lanes_below(bal);
-        if (tk && pos < kWave) {
-          scratch[pos] = composite(zof(q) + 0.0f, idof(q));
-          pend &= ~(1u << q);
-        }
-        base += __popcll(bal);
+  for (int q = 0; q < NQ; ++q) {
+    uint64_t bal = __ballot((pend >> q) & 1u);
+    if (!bal) continue;
+    const uint64_t cq = composite(zof(q) + 0.0f, idof(q));
+    while (bal) {
+      const int src = __ffsll((long long)bal) - 1;
+      bal &= bal - 1;
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)cq, src);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(cq >> 32), src);
+      const uint64_t c = ((uint64_t)hi << 32) | lo;
+      if (c <= kth) continue;
+      best = list_insert(best, c);
+      if (kth != 0ull || list_count(best) >= k) {
+        const uint32_t klo = __builtin_amdgcn_readlane((uint32_t)best, k - 1);
+        const uint32_t khi = __builtin_amdgcn_readlane((uint32_t)(best >> 32), k - 1);
+        kth = ((uint64_t)khi << 32) | klo;
       }
     }
-    wave_lds_sync();
-    const int n = base < kWave ? base : kWave;
-    uint64_t v = lane < n ? scratch[lane] : 0ull;
-    wave_lds_sync();
-    v = wave_sort64_desc(v);
-    best = list_merge(best, v);
-    if (list_count(best) >= k) thr = fmaxf(thr, list_kth_z(best, k));
-    if (pend) {
-#pragma unroll
-      for (int q = 0; q < NQ; ++q)
-        if (((pend >> q) & 1u) && !(zof(q) >= thr)) pend &= ~(1u << q);
-    }
   }
+  if (kth != 0ull) thr = fmaxf(thr, composite_z(kth));
 }
 
 // fp64 finish of a row from its sorted candidate list (lane i = i-th best, n >= 1 entries):
