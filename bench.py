@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sets", type=int, default=0, help="input sets rotated (0 = auto)")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="also run one device-to-device copy of this many bytes (a counter reference)")
     return ap.parse_args()
 
 
@@ -139,6 +141,12 @@ def main():
     kernel_ms = float(per_launch_ms.mean())
     ms_per_step = total_ms / args.steps
     rows_per_s = w.batch / (ms_per_step / 1e3)
+
+    if args.copy_bytes > 0:  # reference kernel of known traffic for rocprofv3 --pmc runs
+        src = torch.empty(args.copy_bytes, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
 
     # sanity: ids are token ids or sentinels
     got = ids[0].cpu().numpy()

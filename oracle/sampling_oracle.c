@@ -36,6 +36,17 @@
 
 #include "../include/arbor_sampling.h"
 
+/* Planted-mistake variants for the tests that pin this oracle (tests/test_oracle_pins.py
+ * builds each with -DORACLE_MUTATION=n and checks that the pins catch it). 0 = the oracle. */
+#ifndef ORACLE_MUTATION
+#define ORACLE_MUTATION 0
+#endif
+#define MUT(n) (ORACLE_MUTATION == (n))
+
+/* id in the low word of the rank key: ~id makes equal z rank by ascending id */
+#define ENC_ID(i) (MUT(3) ? (uint32_t)(i) : ~(uint32_t)(i))
+#define DEC_ID(c) ((int32_t)(MUT(3) ? (uint32_t)(c) : ~(uint32_t)(c)))
+
 /* boundary bits: BOUNDARY_CDF marks a row whose id may legitimately differ from an
  * implementation that agrees with this one to within BOUNDARY_TOL of probability mass;
  * the other two bits only report that the top-p / min-p cut had tokens within
@@ -128,7 +139,7 @@ int oracle_tempered_row(const arbor_sampling_params* p, const void* logits_row,
   for (int i = 0; i < V; i++) {
     float x = p->dtype == ARBOR_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)logits_row)[i])
                                            : ((const float*)logits_row)[i];
-    z[i] = x * inv_t + 0.0f; /* + 0 turns -0 into +0 so that equal values tie on id */
+    z[i] = (MUT(7) ? x / p->temperature : x * inv_t) + 0.0f; /* + 0: -0 becomes +0, equal values tie on id */
   }
   if (p->hist_len > 0 && history_row) {
     int32_t* h = (int32_t*)malloc(sizeof(int32_t) * (size_t)p->hist_len);
@@ -149,18 +160,18 @@ int oracle_tempered_row(const arbor_sampling_params* p, const void* logits_row,
       int e = j;
       while (e < n && h[e] == h[j]) e++;
       const int32_t t = h[j];
-      const float count = (float)(e - j);
+      const float count = MUT(10) ? 1.0f : (float)(e - j);
       float v = z[t];
-      v = v > 0.0f ? v * inv_rp : v * rp;
+      v = v > 0.0f ? v * (MUT(2) ? rp : inv_rp) : v * rp;
       const float pen = count * p->frequency_penalty + p->presence_penalty;
-      z[t] = (v - pen) + 0.0f;
+      z[t] = (MUT(1) ? v + pen : v - pen) + 0.0f;
       j = e;
     }
     free(h);
   }
   if (mask_row) {
     for (int i = 0; i < V; i++)
-      if (!((mask_row[i >> 5] >> (i & 31)) & 1u)) z[i] = -INFINITY;
+      if (!((mask_row[i >> 5] >> (MUT(8) ? 31 - (i & 31) : (i & 31))) & 1u)) z[i] = -INFINITY;
   }
   for (int i = 0; i < V; i++)
     if (isnan(z[i]) || z[i] == INFINITY) return ARBOR_ID_INVALID;
@@ -178,7 +189,8 @@ static void sample_row(const arbor_sampling_params* p, const float* z, float u, 
 
   int64_t nf = 0;
   for (int i = 0; i < V; i++)
-    if (z[i] != -INFINITY) ck[nf++] = ((uint64_t)order_key(z[i]) << 32) | (uint32_t)(~(uint32_t)i);
+    if (z[i] != -INFINITY)
+      ck[nf++] = ((uint64_t)order_key(z[i]) << 32) | ENC_ID(i);
   r.n_finite = (int32_t)nf;
   if (probs_row)
     for (int i = 0; i < V; i++) probs_row[i] = 0.0f;
@@ -198,11 +210,11 @@ static void sample_row(const arbor_sampling_params* p, const float* z, float u, 
   qsort(ck, (size_t)n, sizeof(uint64_t), cmp_u64_desc);
   r.n_topk = (int32_t)n;
 
-  const double zmax = (double)z[~(uint32_t)ck[0]];
+  const double zmax = (double)z[DEC_ID(ck[0])];
   r.max_z = (float)zmax;
   long double ek = 0.0L;
   for (int64_t i = 0; i < n; i++) {
-    e[i] = exp((double)z[~(uint32_t)ck[i]] - zmax);
+    e[i] = exp((double)z[DEC_ID(ck[i])] - zmax);
     ek += e[i];
   }
 
@@ -221,7 +233,7 @@ static void sample_row(const arbor_sampling_params* p, const float* z, float u, 
         r.boundary |= BOUNDARY_TOP_P;
         flip += e[j + 1];
       }
-      if (cut < 0 && frac >= tp) cut = j;
+      if (cut < 0 && (MUT(5) ? frac > tp : frac >= tp)) cut = j;
     }
     lp = cut < 0 ? n : cut + 1;
   }
@@ -237,21 +249,21 @@ static void sample_row(const arbor_sampling_params* p, const float* z, float u, 
         r.boundary |= BOUNDARY_MIN_P;
         flip += e[j];
       }
-      if (e[j] >= mp) lk = j + 1;
+      if ((MUT(9) ? e[j] / (double)ek : e[j]) >= mp) lk = j + 1;
     }
   }
   r.n_kept = (int32_t)lk;
-  r.cut_id = (int32_t)(~(uint32_t)ck[lk - 1]);
+  r.cut_id = DEC_ID(ck[lk - 1]);
   r.cut_z = z[r.cut_id];
 
   /* draw: CDF over the kept set in ascending id order; first C_j > u */
   long double ekept = 0.0L;
   for (int64_t j = 0; j < lk; j++) {
-    kept_ids[j] = (int32_t)(~(uint32_t)ck[j]);
+    kept_ids[j] = DEC_ID(ck[j]);
     ekept += e[j];
   }
   r.kept_mass = (double)ekept;
-  qsort(kept_ids, (size_t)lk, sizeof(int32_t), cmp_i32);
+  if (!MUT(6)) qsort(kept_ids, (size_t)lk, sizeof(int32_t), cmp_i32);
   long double cum = 0.0L;
   int32_t pick = kept_ids[lk - 1]; /* no C_j > u through rounding: the last kept id */
   int found = 0;
@@ -262,7 +274,7 @@ static void sample_row(const arbor_sampling_params* p, const float* z, float u, 
     const double c = (double)(cum / ekept);
     const double gap = fabs(c - (double)u);
     if (gap < r.cdf_gap) r.cdf_gap = gap;
-    if (!found && c > (double)u) {
+    if (!found && (MUT(4) ? c >= (double)u : c > (double)u)) {
       pick = t;
       found = 1;
     }
