@@ -128,7 +128,7 @@ struct Penalty {
 };
 
 // Repetition (once), then frequency * count + presence. One rounding per operation,
-// the same sequence as the oracle; the trailing + 0 turns -0 into +0.
+// the order of operations the contract fixes; the trailing + 0 turns -0 into +0.
 __device__ __forceinline__ float penalize(float z, uint32_t count, const Penalty& p) {
   const float v = z > 0.0f ? z * p.inv_rp : z * p.rp;
   const float pen = (float)count * p.fp + p.pp;
