@@ -40,6 +40,7 @@ struct Args {
   int S, chunk_len;
   int hash_bits, bitmap_words;
   int aligned, write_probs;
+  int pen_mono;  // repetition >= 1, frequency >= 0, presence >= 0: a penalty never raises z
   uint32_t* hdr;   // [B*S*2]            count, flags of each chunk list
   uint64_t* cand;  // [B*S*kChunkSlot]   sorted candidate composites of each chunk
   float* zbuf;     // [B*V]              row solver's tempered logits

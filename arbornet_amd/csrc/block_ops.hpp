@@ -108,14 +108,14 @@ __device__ void block_sort_asc(uint64_t* arr, int n) {
   }
 }
 
-// Sort 64 values held one per lane, descending (bitonic network over shuffles).
+// Sort 64 values held one per lane, descending (bitonic network over DPP / permlane moves).
 __device__ __forceinline__ uint64_t wave_sort64_desc(uint64_t v) {
   const int lane = lane_id();
 #pragma unroll
   for (int size = 2; size <= kWave; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint64_t w = __shfl_xor(v, stride);
+      const uint64_t w = lane_xor_n(v, stride);
       const bool asc = (lane & size) == 0;
       const bool lower = (lane & stride) == 0;
       const uint64_t mx = v > w ? v : w, mn = v > w ? w : v;
@@ -130,7 +130,7 @@ __device__ __forceinline__ uint32_t wave_sort64_desc_u32(uint32_t v) {
   for (int size = 2; size <= kWave; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint32_t w = __shfl_xor(v, stride);
+      const uint32_t w = lane_xor_n(v, stride);
       const bool asc = (lane & size) == 0;
       const bool lower = (lane & stride) == 0;
       const uint32_t mx = v > w ? v : w, mn = v > w ? w : v;

@@ -68,9 +68,9 @@ __device__ float wave_keep_topk(uint64_t* buf, int& n, int k, uint32_t* hist) {
       break;
     }
     const int src = __ffsll((long long)bal) - 1;
-    dsel = __shfl(dsel, src);
-    above = __shfl(above, src);
-    csel = __shfl(csel, src);
+    dsel = lane_get(dsel, src);
+    above = lane_get(above, src);
+    csel = lane_get(csel, src);
     need -= above;
     prefix = (prefix & ~(255ull << shift)) | ((uint64_t)dsel << shift);
     pmask |= 255ull << shift;
@@ -243,7 +243,7 @@ __device__ void gather_prefixes(const Args& a, const uint64_t* lists, int nl, Ld
       const int l = t / h, pos = t % h;
       uint64_t v = (l < nl && pos < s.cnt[l]) ? lists[s.off[l] + pos] : 0ull;
       v = wave_sort64_desc(v);
-      const uint64_t kth = __shfl(v, a.top_k - 1);
+      const uint64_t kth = lane_get(v, a.top_k - 1);
       if (t == 0) s.t0 = kth;
     } else {
       float m = -INFINITY;

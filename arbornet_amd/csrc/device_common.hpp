@@ -48,39 +48,144 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
+// ---------------------------------------------------------------------------------------
+// Cross-lane primitives without LDS: DPP moves inside rows of 16 lanes and the gfx950
+// permlane swaps across rows (v_permlane16_swap / v_permlane32_swap). All of them expect
+// every lane of the wave to be active.
+// ---------------------------------------------------------------------------------------
+template <typename T, typename F>
+__device__ __forceinline__ T map_dwords(T v, F f) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit values");
+  uint32_t d[sizeof(T) / 4];
+  __builtin_memcpy(d, &v, sizeof(T));
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) d[i] = f(d[i], i);
+  T r;
+  __builtin_memcpy(&r, d, sizeof(T));
+  return r;
+}
+
+// DPP move: lanes whose source is outside the row (or whose row is masked off) get `old`.
+template <int CTRL, int ROW_MASK = 0xF, typename T>
+__device__ __forceinline__ T dpp_mov(T old, T v) {
+  uint32_t o[sizeof(T) / 4];
+  __builtin_memcpy(o, &old, sizeof(T));
+  return map_dwords(v, [&](uint32_t x, int i) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)o[i], (int)x, CTRL, ROW_MASK, 0xF, false);
+  });
+}
+constexpr int kDppQuadXor1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppQuadRev = 0x1B;     // quad_perm [3,2,1,0]
+constexpr int kDppRowShr = 0x110;     // + n: row_shr:n
+constexpr int kDppWaveShr1 = 0x138;   // wave_shr:1
+constexpr int kDppRowMirror = 0x140;  // lane 15 - i within the row
+constexpr int kDppHalfMirror = 0x141; // lane 7 - i within the half-row
+constexpr int kDppBcast15 = 0x142;    // lane 15 of the row above
+constexpr int kDppBcast31 = 0x143;    // lane 31
+
+// lo[i] = v[i & ~S], hi[i] = v[i | S] for S = 16 (rows) or 32 (halves).
+template <int S, typename T>
+__device__ __forceinline__ void lane_split(T v, T& lo, T& hi) {
+  uint32_t d[sizeof(T) / 4], l[sizeof(T) / 4], h[sizeof(T) / 4];
+  __builtin_memcpy(d, &v, sizeof(T));
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(T) / 4); ++i) {
+    if constexpr (S == 16) {
+      const auto p = __builtin_amdgcn_permlane16_swap(d[i], d[i], false, false);
+      l[i] = p[0];
+      h[i] = p[1];
+    } else {
+      const auto p = __builtin_amdgcn_permlane32_swap(d[i], d[i], false, false);
+      l[i] = p[0];
+      h[i] = p[1];
+    }
+  }
+  __builtin_memcpy(&lo, l, sizeof(T));
+  __builtin_memcpy(&hi, h, sizeof(T));
+}
+
+// Value of lane (lane ^ J), J a power of two <= 32.
+template <int J, typename T>
+__device__ __forceinline__ T lane_xor(T v) {
+  if constexpr (J == 1) {
+    return dpp_mov<kDppQuadXor1>(v, v);
+  } else if constexpr (J == 2) {
+    return dpp_mov<kDppQuadXor2>(v, v);
+  } else if constexpr (J == 4) {
+    return dpp_mov<kDppQuadRev>(v, dpp_mov<kDppHalfMirror>(v, v));  // (i ^ 7) ^ 3
+  } else if constexpr (J == 8) {
+    return dpp_mov<kDppHalfMirror>(v, dpp_mov<kDppRowMirror>(v, v));  // (i ^ 15) ^ 7
+  } else {
+    static_assert(J == 16 || J == 32, "power of two <= 32");
+    T lo, hi;
+    lane_split<J>(v, lo, hi);
+    return (lane_id() & J) ? lo : hi;
+  }
+}
+// lane_xor with a stride known only after unrolling
+template <typename T>
+__device__ __forceinline__ T lane_xor_n(T v, int j) {
+  switch (j) {
+    case 1: return lane_xor<1>(v);
+    case 2: return lane_xor<2>(v);
+    case 4: return lane_xor<4>(v);
+    case 8: return lane_xor<8>(v);
+    case 16: return lane_xor<16>(v);
+    default: return lane_xor<32>(v);
+  }
+}
+// Value of lane 63 - lane.
+template <typename T>
+__device__ __forceinline__ T lane_reverse(T v) {
+  return lane_xor<32>(lane_xor<16>(dpp_mov<kDppRowMirror>(v, v)));
+}
+// Value of lane `src` (wave-uniform) in every lane.
+template <typename T>
+__device__ __forceinline__ T lane_get(T v, int src) {
+  return map_dwords(v, [&](uint32_t x, int) { return (uint32_t)__builtin_amdgcn_readlane((int)x, src); });
+}
+// Value of lane - 1 (lane 0 gets `fill`).
+template <typename T>
+__device__ __forceinline__ T lane_shift_down(T v, T fill) {
+  return dpp_mov<kDppWaveShr1>(fill, v);
+}
+
+// Butterfly reduction; every lane gets the result, bitwise identical in every lane.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+  v = op(v, lane_xor<1>(v));
+  v = op(v, lane_xor<2>(v));
+  v = op(v, dpp_mov<kDppHalfMirror>(v, v));
+  v = op(v, dpp_mov<kDppRowMirror>(v, v));
+  T lo, hi;
+  lane_split<16>(v, lo, hi);
+  v = op(lo, hi);
+  lane_split<32>(v, lo, hi);
+  return op(lo, hi);
+}
 template <typename T>
 __device__ __forceinline__ T wave_max(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const T w = __shfl_xor(v, o);
-    v = w > v ? w : v;
-  }
-  return v;
+  return wave_reduce(v, [](T x, T y) { return y > x ? y : x; });
 }
 template <typename T>
 __device__ __forceinline__ T wave_min(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const T w = __shfl_xor(v, o);
-    v = w < v ? w : v;
-  }
-  return v;
+  return wave_reduce(v, [](T x, T y) { return y < x ? y : x; });
 }
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  return wave_reduce(v, [](T x, T y) { return x + y; });
 }
 // Inclusive prefix sum across the wave in lane order.
 template <typename T>
 __device__ __forceinline__ T wave_scan_incl(T v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const T w = __shfl_up(v, o);
-    if (lane >= o) v += w;
-  }
+  const T z = T(0);
+  v = v + dpp_mov<kDppRowShr + 1>(z, v);
+  v = v + dpp_mov<kDppRowShr + 2>(z, v);
+  v = v + dpp_mov<kDppRowShr + 4>(z, v);
+  v = v + dpp_mov<kDppRowShr + 8>(z, v);
+  v = v + dpp_mov<kDppBcast15, 0xA>(z, v);
+  v = v + dpp_mov<kDppBcast31, 0xC>(z, v);
   return v;
 }
 

@@ -128,7 +128,7 @@ __device__ CutResult radix_cut(const float* z, int V, float zmax, bool by_mass, 
 // The full contract for one row, by one workgroup of BLOCK threads. htab has
 // 1 << a.hash_bits slots of LDS.
 template <int BLOCK, int DT>
-__device__ void solve_row(const Args& a, int row, uint32_t* htab, SolverShared& sh) {
+__device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab, SolverShared& sh) {
   const int t = threadIdx.x;
   const int V = a.V;
   float* z = a.zbuf + (size_t)row * (size_t)V;

@@ -120,7 +120,7 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
     // raise the threshold from this batch's lane maxima
     if (MODE_K) {
       const uint32_t key = wave_sort64_desc_u32(order_key(lmax));
-      thr = fmaxf(thr, key_value(__shfl(key, a.top_k - 1)));
+      thr = fmaxf(thr, key_value(lane_get(key, a.top_k - 1)));
     } else {
       const float m = wave_max(lmax);
       if (m > -INFINITY) thr = fmaxf(thr, m + a.ln_min_p_lo);
@@ -193,7 +193,7 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
   auto grab = [&]() -> int {
     int b = 0;
     if (lane == 0) b = atomicAdd(&s.next_batch, 1);
-    return __shfl(b, 0);
+    return lane_get(b, 0);
   };
   Batch ba, bb;
   int bi = grab();
@@ -550,7 +550,7 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   auto grab = [&]() -> int {
     int b = 0;
     if (lane == 0) b = atomicAdd(&s.next_batch, 1);
-    return __shfl(b, 0);
+    return lane_get(b, 0);
   };
   __syncthreads();  // the sample histogram is no longer read: wave radix histograms may reuse it
   auto process = [&](int b, const Batch& bt) {

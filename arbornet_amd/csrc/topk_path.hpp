@@ -20,11 +20,11 @@ constexpr int kListSlots = kWaves;  // one list per wave
 // Top-64 of two descending lists (lane i holds the i-th entry), descending.
 __device__ __forceinline__ uint64_t list_merge(uint64_t a, uint64_t b) {
   const int lane = lane_id();
-  const uint64_t rb = __shfl(b, kWave - 1 - lane);
+  const uint64_t rb = lane_reverse(b);
   uint64_t v = a > rb ? a : rb;  // bitonic, holds the 64 best of a and b
 #pragma unroll
   for (int stride = kWave / 2; stride > 0; stride >>= 1) {
-    const uint64_t w = __shfl_xor(v, stride);
+    const uint64_t w = lane_xor_n(v, stride);
     const bool lower = (lane & stride) == 0;
     const uint64_t mx = v > w ? v : w, mn = v > w ? w : v;
     v = lower ? mx : mn;
@@ -35,14 +35,10 @@ __device__ __forceinline__ uint64_t list_merge(uint64_t a, uint64_t b) {
 __device__ __forceinline__ int list_count(uint64_t v) { return __popcll(__ballot(v != 0ull)); }
 
 // z of entry k-1 of a list with at least k entries
-__device__ __forceinline__ float list_kth_z(uint64_t v, int k) { return composite_z(__shfl(v, k - 1)); }
+__device__ __forceinline__ float list_kth_z(uint64_t v, int k) { return composite_z(lane_get(v, k - 1)); }
 
 // The list shifted down by one lane (lane i gets lane i-1; DPP wave_shr:1, no LDS).
-__device__ __forceinline__ uint64_t list_shift_down(uint64_t v) {
-  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, 0x138, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), 0x138, 0xF, 0xF, false);
-  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
-}
+__device__ __forceinline__ uint64_t list_shift_down(uint64_t v) { return lane_shift_down(v, (uint64_t)0); }
 
 // Insert composite c (wave-uniform) into a descending list, dropping the 64th entry.
 __device__ __forceinline__ uint64_t list_insert(uint64_t best, uint64_t c) {
@@ -57,7 +53,7 @@ __device__ __forceinline__ uint64_t list_insert(uint64_t best, uint64_t c) {
 // once the list holds k. `thr` tracks the k-th z. Wave-uniform control flow.
 template <int NQ, typename ZOf, typename IdOf>
 __device__ __forceinline__ void list_absorb(uint64_t& best, float& thr, int k, uint32_t pend, ZOf zof, IdOf idof) {
-  uint64_t kth = list_count(best) >= k ? __shfl(best, k - 1) : 0ull;
+  uint64_t kth = list_count(best) >= k ? lane_get(best, k - 1) : 0ull;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     uint64_t bal = __ballot((pend >> q) & 1u);
@@ -84,15 +80,15 @@ __device__ __forceinline__ void list_absorb(uint64_t& best, float& thr, int k, u
 // fp64 finish of a row from its sorted candidate list (lane i = i-th best, n >= 1 entries):
 // top-p, then min-p, then the first id (ascending) whose running mass exceeds u * E.
 // One wave; writes out_ids[row] and, if asked, the kept probabilities.
-__device__ void finish_list(const Args& a, int row, uint64_t best, int n) {
+__device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t best, int n) {
   const int lane = lane_id();
   const bool in = lane < n;
-  const double z0 = (double)composite_z(__shfl(best, 0));
+  const double z0 = (double)composite_z(lane_get(best, 0));
   const double e = in ? exp((double)composite_z(best) - z0) : 0.0;
   const double cum = wave_scan_incl(e);
   int lp = n;
   if (a.top_p < 1.0f) {
-    const double target = (double)a.top_p * __shfl(cum, n - 1);
+    const double target = (double)a.top_p * lane_get(cum, n - 1);
     const uint64_t hit = __ballot(in && cum >= target);
     if (hit) lp = __ffsll((long long)hit);
   }
@@ -109,11 +105,11 @@ __device__ void finish_list(const Args& a, int row, uint64_t best, int n) {
   const double er = __shfl(e, lane < kept ? r : 0);
   const double w = lane < kept ? er : 0.0;
   const double cid = wave_scan_incl(w);
-  const double E = __shfl(cid, kept - 1);
+  const double E = lane_get(cid, kept - 1);
   const double target = (double)a.uniforms[row] * E;
   const uint64_t over = __ballot(lane < kept && cid > target);
   const int pick = over ? __ffsll((long long)over) - 1 : kept - 1;
-  const int32_t pick_id = (int32_t)(__shfl(key, pick) >> 32);
+  const int32_t pick_id = (int32_t)(lane_get(key, pick) >> 32);
   if (lane == 0) a.out_ids[row] = pick_id;
   if (a.write_probs && lane < kept) a.out_probs[(size_t)row * (size_t)a.V + (key >> 32)] = (float)(er / E);
 }
