@@ -32,6 +32,7 @@ struct Args {
   int32_t* out_ids;
   float* out_probs;
   float inv_t;
+  float temp;  // temperature (raw-logit thresholds)
   Penalty pen;
   int top_k;          // 0 = off (k >= V is off)
   float top_p;        // 1 = off

@@ -20,7 +20,7 @@ namespace arbor {
 // everything the wave sees afterwards. MSB-first radix select, 8-bit digits taken just
 // below the highest bit in which the entries differ.
 template <int CAP>
-__device__ float wave_keep_topk(uint64_t* buf, int& n, int k, uint32_t* hist) {
+__device__ __forceinline__ float wave_keep_topk(uint64_t* buf, int& n, int k, uint32_t* hist) {
   const int lane = lane_id();
   uint64_t lo = ~0ull, hi = 0;
   for (int i = lane; i < n; i += kWave) {
@@ -99,7 +99,7 @@ __device__ float wave_keep_topk(uint64_t* buf, int& n, int k, uint32_t* hist) {
     nn += __popcll(bal);
   }
   wave_lds_sync();
-  n = nn;
+  n = uniform<int>(nn);
   mn = wave_min(mn);
   return nn > 0 ? composite_z(mn) : -FLT_MAX;
 }

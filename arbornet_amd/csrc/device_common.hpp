@@ -140,6 +140,17 @@ template <typename T>
 __device__ __forceinline__ T lane_reverse(T v) {
   return lane_xor<32>(lane_xor<16>(dpp_mov<kDppRowMirror>(v, v)));
 }
+// A wave-uniform value, marked as such for the compiler (kept in a scalar register).
+template <typename T>
+__device__ __forceinline__ T uniform(T v) {
+  static_assert(sizeof(T) == 4, "32-bit values");
+  int i;
+  __builtin_memcpy(&i, &v, 4);
+  i = __builtin_amdgcn_readfirstlane(i);
+  __builtin_memcpy(&v, &i, 4);
+  return v;
+}
+
 // Value of lane `src` (wave-uniform) in every lane.
 template <typename T>
 __device__ __forceinline__ T lane_get(T v, int src) {

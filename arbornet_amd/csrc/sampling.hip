@@ -263,120 +263,124 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Streaming top-k (1 <= k <= 64)
+// Streaming top-k (1 <= k <= 64): one workgroup per row, or per chunk of a row.
 //
-//  A. Threshold: the k-th best of the 1024 lane maxima of every wave's first two batches
-//     is a lower bound T0 of the row's k-th best (the k-th best of a subset never exceeds
-//     the k-th best of the whole); it is found with one 2048-bin histogram over the keys'
-//     observed range, taking the lower edge of the bin that holds the k-th maximum.
-//  B. Stream: everything >= the wave's threshold (T0, raised by an exact wave radix
-//     select if the wave's buffer fills) is appended to a per-wave LDS buffer.
-//  C. Select: the wave buffers and the penalised history ids >= T0 form the union; a block
-//     radix select finds its k-th best; one wave sorts the k survivors and draws (fp64).
+//  Set-up: the row's history ids are loaded ahead of the logits and fill an LDS bitmap of
+//     the chunk's history ids and an id -> count table while the first two batches of
+//     every wave are in flight.
+//  A. Threshold: T0 is a lower bound of the k-th largest of the 1024 lane maxima of every
+//     wave's first two batches (the k-th largest of a subset never exceeds the k-th
+//     largest of the whole): a histogram of the order keys' top 10 bits, then of the next
+//     10 bits inside the bin that holds the k-th; every wave reads the bins itself.
+//  B. Stream: everything >= the wave's threshold is appended to a per-wave LDS buffer; a
+//     full buffer is cut to its exact k best (wave radix select), raising the threshold.
+//     When no penalty can raise a logit (repetition >= 1, frequency and presence >= 0)
+//     history ids stream past like the others and only those whose raw z passes are
+//     penalised; otherwise they are skipped and scored once at set-up.
+//  C. Finish: each wave sorts its k best (bitonic network over DPP), a tree of bitonic
+//     merges (four barriers) leaves the chunk's k best in wave 0, which draws in fp64 or
+//     publishes them for the row's finish kernel.
 // ---------------------------------------------------------------------------------------
-constexpr int kTopkWaveCap = 256;   // candidates one wave buffers
-constexpr int kUnionCap = 4096;     // candidates the row's selection runs over
-constexpr int kSampleBins = 2048;   // histogram bins of the threshold sample
+constexpr int kTopkWaveCap = 256;  // candidates one wave buffers
+constexpr int kBinBits = 10;       // threshold histograms: 2 x 10 bits of the order key
+constexpr int kBins = 1 << kBinBits;
+#ifndef TOPK_UNROLL_F32
+#define TOPK_UNROLL_F32 3
+#endif
+#ifndef TOPK_SAMPLE_BOTH
+#define TOPK_SAMPLE_BOTH 1
+#endif
+
+// Counts of 10-bit key digits with a 64-bin summary (16 bins each), so that the bin of
+// the need-th largest entry is found with two wave scans.
+struct KeyHist {
+  uint32_t fine[kBins];
+  uint32_t coarse[kBins / 16];
+};
+__device__ __forceinline__ void key_hist_add(KeyHist& h, uint32_t bin) {
+  atomicAdd(&h.fine[bin], 1u);
+  atomicAdd(&h.coarse[bin >> 4], 1u);
+}
+// Bin holding the need-th largest entry (1 <= need <= total), counted from the top bin
+// down; *above = entries in higher bins. Every lane of the wave gets the result.
+__device__ __forceinline__ int key_hist_kth(const KeyHist& h, uint32_t need, uint32_t* above) {
+  static_assert(kBins / 16 == kWave, "one summary bin per lane");
+  const int lane = lane_id();
+  const uint32_t cc = h.coarse[kWave - 1 - lane];  // lane l: l-th highest summary bin
+  const uint32_t ci = wave_scan_incl(cc);
+  const uint64_t hit = __ballot(ci >= need);
+  if (!hit) {
+    *above = lane_get(ci, kWave - 1);
+    return 0;
+  }
+  const int lc = __ffsll((long long)hit) - 1;
+  const uint32_t base = lane_get(ci - cc, lc);
+  const int cbin = kWave - 1 - lc;
+  const uint32_t cf = lane < 16 ? h.fine[cbin * 16 + 15 - lane] : 0u;
+  const uint32_t fi = wave_scan_incl(cf);
+  const int lf = __ffsll((long long)__ballot(lane < 16 && base + fi >= need)) - 1;
+  *above = base + lane_get(fi - cf, lf);
+  return cbin * 16 + 15 - lf;
+}
+
+// 16-byte loads per lane per batch of the streaming top-k kernel (two batches in flight)
+template <int DT>
+struct TopkUnroll {
+  static constexpr int value = DT == ARBOR_DTYPE_F32 ? TOPK_UNROLL_F32 : 2;
+};
 
 struct TopkShared {
   int next_batch;
   uint32_t flags;
-  int n_union;
-  int n_top;
-  float t0;
-  int dsel;
-  uint32_t above, csel;
-  int cnt[kWaves];
-  int off[kWaves + 1];
-  uint32_t red[kWaves];
-  uint64_t red64[kWaves];
+  int n_hc;   // penalised history candidates in hc[] (history scored at set-up)
+  int n_sel;  // entries at or above the final selection's bin edge
 };
 
-// Dynamic LDS of topk_kernel (bytes): wave buffers | histograms | chunk bitmap |
-// history candidates | history table (later the union).
+// Dynamic LDS of topk_kernel (bytes): wave buffers | radix histograms | threshold
+// histograms | chunk bitmap | history candidates | history table.
 struct TopkLds {
-  uint64_t* wb;      // [kWaves * kTopkWaveCap]
-  uint32_t* hist;    // [kWaves * 256] (also the 2048-bin sample histogram; solver scratch)
+  uint64_t* wb;      // [kWaves * kTopkWaveCap]; at the end the waves' sorted lists
+  uint32_t* hist;    // [kWaves * 256] wave radix histograms (row solver scratch on fallback)
+  KeyHist* kh;       // [4] threshold sample (two levels), final selection (two levels)
+  uint64_t* sel;     // [kWave] the chunk's k best, unordered
+  uint64_t* side;    // [kWaves * kWave] history ids whose raw z passed (penalised at the end)
   uint32_t* bitmap;  // [bitmap_words]
-  uint64_t* hc;      // [hist_len] penalised history candidates
-  uint32_t* htab;    // [1 << hash_bits], then overlaid by
-  uint64_t* uni;     // [kUnionCap]
+  uint64_t* hc;      // [hist_len] penalised history candidates (history scored at set-up)
+  uint32_t* htab;    // [hash_slots]
   __host__ __device__ static size_t bytes(int bitmap_words, int hist_len, int hash_slots) {
-    const size_t tail = sizeof(uint32_t) * (size_t)hash_slots > sizeof(uint64_t) * kUnionCap
-                            ? sizeof(uint32_t) * (size_t)hash_slots
-                            : sizeof(uint64_t) * kUnionCap;
-    return sizeof(uint64_t) * kWaves * kTopkWaveCap + sizeof(uint32_t) * kWaves * 256 +
-           (sizeof(uint32_t) * (size_t)bitmap_words + 7) / 8 * 8 + sizeof(uint64_t) * (size_t)hist_len + tail;
+    return sizeof(uint64_t) * kWaves * (kTopkWaveCap + kWave) + sizeof(uint32_t) * kWaves * 256 +
+           sizeof(KeyHist) * 4 + sizeof(uint64_t) * kWave + (sizeof(uint32_t) * (size_t)bitmap_words + 7) / 8 * 8 +
+           sizeof(uint64_t) * (size_t)hist_len + sizeof(uint32_t) * (size_t)hash_slots;
   }
   __device__ TopkLds(unsigned char* base, int bitmap_words, int hist_len) {
     wb = reinterpret_cast<uint64_t*>(base);
-    hist = reinterpret_cast<uint32_t*>(wb + kWaves * kTopkWaveCap);
-    bitmap = hist + kWaves * 256;
+    side = wb + kWaves * kTopkWaveCap;
+    hist = reinterpret_cast<uint32_t*>(side + kWaves * kWave);
+    kh = reinterpret_cast<KeyHist*>(hist + kWaves * 256);
+    sel = reinterpret_cast<uint64_t*>(kh + 4);
+    bitmap = reinterpret_cast<uint32_t*>(sel + kWave);
     hc = reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(bitmap) +
                                      ((size_t)bitmap_words * sizeof(uint32_t) + 7) / 8 * 8);
     htab = reinterpret_cast<uint32_t*>(hc + hist_len);
-    uni = reinterpret_cast<uint64_t*>(htab);
   }
 };
-
-// Composite T such that exactly min(k, n) of the n distinct composites u[0, n) are >= T:
-// MSB-first radix select, 8-bit digits below the highest bit in which they differ.
-template <int BLOCK>
-__device__ uint64_t block_select_kth(const uint64_t* u, int n, int k, uint32_t* hist, TopkShared& s) {
-  const int t = threadIdx.x;
-  if (n <= k) return 0ull;
-  uint64_t lo = ~0ull, hi = 0ull;
-  for (int i = t; i < n; i += BLOCK) {
-    lo = u[i] < lo ? u[i] : lo;
-    hi = u[i] > hi ? u[i] : hi;
-  }
-  lo = block_reduce_min<BLOCK, uint64_t>(lo, s.red64);
-  hi = block_reduce_max<BLOCK, uint64_t>(hi, s.red64);
-  const int hb = 63 - __clzll(hi ^ lo);
-  int shift = hb >= 7 ? hb - 7 : 0;
-  uint64_t pmask = hb >= 63 ? 0ull : (~0ull << (hb + 1));
-  uint64_t prefix = hi & pmask;
-  uint32_t need = (uint32_t)k;
-  for (;;) {
-    if (t < 256) hist[t] = 0u;
-    __syncthreads();
-    for (int i = t; i < n; i += BLOCK) {
-      const uint64_t c = u[i];
-      if ((c & pmask) == prefix) atomicAdd(&hist[(uint32_t)(c >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    const uint32_t cnt = t < 256 ? hist[255 - t] : 0u;  // descending digits
-    uint32_t tot;
-    const uint32_t ex = block_scan_excl<BLOCK, uint32_t>(cnt, s.red, &tot);
-    if (t < 256 && ex < need && ex + cnt >= need) {
-      s.dsel = 255 - t;
-      s.above = ex;
-      s.csel = cnt;
-    }
-    __syncthreads();
-    const int dsel = s.dsel;
-    const uint32_t above = s.above, csel = s.csel;
-    __syncthreads();
-    need -= above;
-    prefix = (prefix & ~(255ull << shift)) | ((uint64_t)dsel << shift);
-    pmask |= 255ull << shift;
-    if (need == csel || shift == 0) return prefix;
-    shift = shift >= 8 ? shift - 8 : 0;
-  }
-}
 
 template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED>
 __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   constexpr int VEC = Elem<DT>::kVec;
-  constexpr int U = Elem<DT>::kUnroll;
+  constexpr int U = TopkUnroll<DT>::value;
   constexpr int NQ = VEC * U;                       // elements per lane per batch
   constexpr int kBatch = U * kWave;                 // units per batch
   constexpr int HR = (1 << kMaxHashBits) / kBlock;  // history-table slots per thread
   constexpr int HIDR = (ARBOR_HISTORY_MAX + kBlock - 1) / kBlock;
+  static_assert(sizeof(SolverShared) <= sizeof(uint32_t) * kWaves * 256, "solver scratch fits the radix histograms");
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ TopkShared s;
-  const bool own_hist = PEN && (blockIdx.x % a.S) == 0;  // this workgroup evaluates the row's history
-  TopkLds L(smem, PEN ? a.bitmap_words : 0, own_hist ? a.H : 0);
+  // history ids stream past and are penalised inline, or are scored here at set-up by
+  // the first chunk of the row
+  const bool hist_inline = PEN && a.pen_mono;
+  const bool own_hist = PEN && !hist_inline && (blockIdx.x % a.S) == 0;
+  TopkLds L(smem, PEN ? a.bitmap_words : 0, PEN && !a.pen_mono ? a.H : 0);
 
   const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
   const int row = blockIdx.x / a.S, chunk = blockIdx.x % a.S;
@@ -416,10 +420,9 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
       }
     }
   };
-  // tempered logit of slot q of batch b; history ids (scored separately, penalised),
-  // masked ids and units past the chunk read as -inf; NaN / +inf read as -inf (flagged
-  // by `process`)
-  auto zof = [&](int b, const Batch& bt, int q) -> float {
+  // tempered logit of slot q of batch b for the threshold sample: history ids, masked ids,
+  // units past the chunk and NaN / +inf read as -inf (the sample leaves them out)
+  auto zsample = [&](int b, const Batch& bt, int q) -> float {
     const int u = q / VEC, j = q % VEC;
     const int unit = b * kBatch + u * kWave + lane;
     const int e0 = c0 + unit * VEC;
@@ -430,30 +433,32 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
     return is_invalid(v) ? -INFINITY : v;
   };
 
-  // two batches per wave are in flight while the workgroup sets up
-  Batch ba, bb;
-  int ia = wave, ib = wave + kWaves;
-  load(ia, ba);
-  load(ib, bb);
-
+  // history ids first, so that the set-up waits for them and not for the logits
   int32_t hid[HIDR];
   if (PEN) {
     const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
 #pragma unroll
     for (int r = 0; r < HIDR; ++r) {
       const int j = t + r * kBlock;
-      hid[r] = j < a.H ? h[j] : -1;
+      const int32_t v = h[j < a.H ? j : a.H - 1];  // every lane loads: the loads in flight stay countable
+      hid[r] = j < a.H ? v : -1;
     }
   }
+  // two batches per wave are in flight while the workgroup sets up
+  Batch ba, bb;
+  int ia = wave, ib = wave + kWaves;
+  load(ia, ba);
+  load(ib, bb);
+
   if (t == 0) {
     s.next_batch = 2 * kWaves;
     s.flags = 0u;
-    s.n_union = 0;
-    s.n_top = 0;
+    s.n_hc = 0;
   }
+  for (int i = t; i < (int)(4 * sizeof(KeyHist) / 4); i += kBlock) reinterpret_cast<uint32_t*>(L.kh)[i] = 0u;
   if (PEN) {
     for (int i = t; i < a.bitmap_words; i += kBlock) L.bitmap[i] = 0u;
-    if (own_hist)
+    if (own_hist || hist_inline)
       for (int i = t; i < (1 << a.hash_bits); i += kBlock) L.htab[i] = kEmptySlot;
   }
   if (a.write_probs) {
@@ -470,7 +475,7 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
         bad = true;
       } else if (id >= 0) {
         if (id >= c0 && id < c1) atomicOr(&L.bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
-        if (own_hist) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
+        if (own_hist || hist_inline) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
       }
     }
     if (bad) atomicOr(&s.flags, kFlagBadHistory);
@@ -501,117 +506,166 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
       if (is_invalid(z)) {
         bad = true;
       } else if (z != -INFINITY) {
-        L.hc[atomicAdd(&s.n_top, 1)] = composite(z, idq[r]);  // n_top counts hc[] here
+        L.hc[atomicAdd(&s.n_hc, 1)] = composite(z, idq[r]);
       }
     }
   }
 
   // ---- A. threshold from the lane maxima of the first two batches ----
+  float t0;
   {
     float lm = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zof(ia, ba, q));
+    for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zsample(ia, ba, q));
+#if TOPK_SAMPLE_BOTH
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zof(ib, bb, q));
-    const uint32_t key = order_key(lm);
-    const uint32_t kmin = block_reduce_min<kBlock, uint32_t>(key, s.red);
-    const uint32_t kmax = block_reduce_max<kBlock, uint32_t>(key, s.red);
-    const uint32_t span = kmax - kmin;
-    const int sh = span == 0u ? 0 : max(0, 32 - __clz(span) - 11);
-    for (int i = t; i < kSampleBins; i += kBlock) L.hist[i] = 0u;
+    for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zsample(ib, bb, q));
+#endif
+    const uint32_t key = order_key(lm + 0.0f);
+    key_hist_add(L.kh[0], key >> (32 - kBinBits));
     __syncthreads();
-    atomicAdd(&L.hist[(key - kmin) >> sh], 1u);
+    uint32_t above1, above2;
+    const int b1 = key_hist_kth(L.kh[0], (uint32_t)k, &above1);
+    if ((int)(key >> (32 - kBinBits)) == b1) key_hist_add(L.kh[1], (key >> (32 - 2 * kBinBits)) & (kBins - 1));
     __syncthreads();
-    // bins in descending order, two per thread
-    const uint32_t h0 = L.hist[kSampleBins - 1 - 2 * t], h1 = L.hist[kSampleBins - 2 - 2 * t];
-    uint32_t tot;
-    const uint32_t ex = block_scan_excl<kBlock, uint32_t>(h0 + h1, s.red, &tot);
-    if (t == 0) s.t0 = -FLT_MAX;
-    __syncthreads();
-    int bsel = -1;
-    if (ex < (uint32_t)k && ex + h0 >= (uint32_t)k)
-      bsel = kSampleBins - 1 - 2 * t;
-    else if (ex + h0 < (uint32_t)k && ex + h0 + h1 >= (uint32_t)k)
-      bsel = kSampleBins - 2 - 2 * t;
-    if (bsel >= 0) {
-      const float tz = key_value(kmin + ((uint32_t)bsel << sh));
-      s.t0 = tz > -FLT_MAX ? tz : -FLT_MAX;
-    }
-    __syncthreads();
+    const int b2 = key_hist_kth(L.kh[1], (uint32_t)k - above1, &above2);
+    // lower edge of the bin: no key in it is smaller; -inf / NaN edges become -FLT_MAX
+    t0 = fmaxf(key_value(((uint32_t)b1 << (32 - kBinBits)) | ((uint32_t)b2 << (32 - 2 * kBinBits))), -FLT_MAX);
   }
-  const float t0 = s.t0;
 
   // ---- B. stream: batches from an LDS counter, two in flight per wave ----
   uint64_t* buf = L.wb + wave * kTopkWaveCap;
   uint32_t* rh = L.hist + wave * 256;
-  int wc = 0;
-  float thr = t0;  // append z >= thr
+  uint64_t* side = L.side + wave * kWave;
+  int wc = 0, nside = 0;
+  // append z >= thr. The raw test x >= x_thr is implied by z = fl(x * (1/T)) >= thr
+  // (x_thr = thr * T lowered by a relative and an absolute margin), so the hot loop
+  // compares raw logits and computes z only for the few that pass.
+  float thr = 0.0f, x_thr = 0.0f;
+  auto set_thr = [&](float t) {
+    thr = uniform(t);
+    const float tt = thr * a.temp;
+    x_thr = uniform(tt - (fabsf(tt) * 0x1p-20f + 0x1p-120f));
+  };
+  set_thr(t0);
   bool ovf = false;
   auto grab = [&]() -> int {
     int b = 0;
     if (lane == 0) b = atomicAdd(&s.next_batch, 1);
     return lane_get(b, 0);
   };
-  __syncthreads();  // the sample histogram is no longer read: wave radix histograms may reuse it
+  auto id_of = [&](int b, int q) { return c0 + (b * kBatch + (q / VEC) * kWave + lane) * VEC + (q % VEC); };
+  // element q of a batch is past the chunk or masked (mw: its unit's mask word)
+  auto dropped_w = [&](int b, int q, uint32_t mw) -> bool {
+    const int unit = b * kBatch + (q / VEC) * kWave + lane;
+    if (unit >= n_units) return true;
+    return MASK && !((mw >> (((c0 + unit * VEC) & 31) + (q % VEC))) & 1u);
+  };
+  auto in_history = [&](int b, int q) -> bool {
+    const int off = (b * kBatch + (q / VEC) * kWave + lane) * VEC;
+    return PEN && ((L.bitmap[off >> 5] >> ((off & 31) + (q % VEC))) & 1u);
+  };
+  // one candidate (its lane passed the raw test): z, or -inf if not taken (history ids
+  // scored at set-up are not taken here)
+  auto candidate = [&](int b, int q, float x, uint32_t mw) -> float {
+    if (dropped_w(b, q, mw)) return -INFINITY;
+    const float v = x * a.inv_t;
+    if (is_invalid(v)) {
+      bad = true;  // +inf, or overflow to +inf
+      return -INFINITY;
+    }
+    if (PEN && !hist_inline && in_history(b, q)) return -INFINITY;
+    return v;
+  };
+  auto append = [&](uint64_t* dst, int& n, bool tk, float v, int id) {
+    const uint64_t m = __ballot(tk);
+    if (tk) dst[n + lanes_below(m)] = composite(v + 0.0f, id);
+    n = uniform<int>(n + __popcll(m));
+  };
   auto process = [&](int b, const Batch& bt) {
-    uint32_t pend = 0u;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int unit = b * kBatch + u * kWave + lane;
-      const int e0 = c0 + unit * VEC;
-      const bool valid = unit < n_units;
-      const uint32_t mb = MASK ? bt.mw[u] >> (e0 & 31) : ~0u;
-      const uint32_t pb = PEN && valid ? L.bitmap[(e0 - c0) >> 5] >> ((e0 - c0) & 31) : 0u;
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        const float v = unpack_unit<DT>(bt.w[u], j) * a.inv_t;
-        const bool skip = !valid || (PEN && ((pb >> j) & 1u)) || (MASK && !((mb >> j) & 1u));
-        bad |= !skip && is_invalid(v);
-        if (!skip && v >= thr && !is_invalid(v)) pend |= 1u << (u * VEC + j);
-      }
-    }
-    if (!__ballot(pend != 0u) || ovf) return;
-    int cnt = wave_sum((int)__popc(pend));
-    if (wc + cnt > kTopkWaveCap) {
-      if (wc > k) thr = fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh));
-#pragma unroll
-      for (int q = 0; q < NQ; ++q)
-        if (((pend >> q) & 1u) && !(zof(b, bt, q) >= thr)) pend &= ~(1u << q);
-      cnt = wave_sum((int)__popc(pend));
-      if (wc + cnt > kTopkWaveCap) {
-        // a batch denser than the buffer: 64 candidates at a time, an exact prune between
-#pragma unroll 1
-        for (int q = 0; q < NQ; ++q) {
-          float v = -INFINITY;
-#pragma unroll
-          for (int qq = 0; qq < NQ; ++qq)
-            if (qq == q && ((pend >> qq) & 1u)) v = zof(b, bt, qq);
-          if (!__ballot(v >= thr)) continue;
-          if (wc + kWave > kTopkWaveCap) {
-            thr = fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh));
-            if (wc + kWave > kTopkWaveCap) {
-              ovf = true;  // unreachable for k <= 64: the row would go to the row solver
-              return;
-            }
-          }
-          const bool take = v >= thr;
-          const uint64_t bal = __ballot(take);
-          if (take) buf[wc + lanes_below(bal)] =
-              composite(v + 0.0f, c0 + (b * kBatch + (q / VEC) * kWave + lane) * VEC + (q % VEC));
-          wc += __popcll(bal);
-        }
-        return;
-      }
-    }
+    uint64_t bal[NQ];
+    uint64_t any = 0ull, nanm = 0ull;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      const bool tk = (pend >> q) & 1u;
-      const uint64_t bal = __ballot(tk);
-      if (bal) {
-        if (tk)
-          buf[wc + lanes_below(bal)] =
-              composite(zof(b, bt, q) + 0.0f, c0 + (b * kBatch + (q / VEC) * kWave + lane) * VEC + (q % VEC));
-        wc += __popcll(bal);
+      const float x = unpack_unit<DT>(bt.w[q / VEC], q % VEC);
+      if (MASK) {  // masked ids never pass (most ids of a constrained row are masked)
+        const int e = c0 + (b * kBatch + (q / VEC) * kWave + lane) * VEC;
+        bal[q] = __ballot(x >= x_thr && ((bt.mw[q / VEC] >> ((e & 31) + (q % VEC))) & 1u));
+      } else {
+        bal[q] = __ballot(x >= x_thr);
+      }
+      any |= bal[q];
+      nanm |= __ballot(x != x);
+    }
+    if (nanm) {  // rare: a NaN counts unless masked or past the chunk
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const float x = unpack_unit<DT>(bt.w[q / VEC], q % VEC);
+        if (x != x && !dropped_w(b, q, MASK ? bt.mw[q / VEC] : 0u)) bad = true;
+      }
+    }
+    if (!any) return;
+    int cnt = 0;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) cnt += __popcll(bal[q]);
+    if (wc + cnt <= kTopkWaveCap) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        if (!bal[q]) continue;
+        bool tk = (bal[q] >> lane) & 1ull;
+        float v = -INFINITY;
+        if (tk) {
+          v = candidate(b, q, unpack_unit<DT>(bt.w[q / VEC], q % VEC), MASK ? bt.mw[q / VEC] : 0u);
+          tk = v >= thr;
+        }
+        const bool hist = hist_inline && tk && in_history(b, q);  // set aside, penalised at the end
+        append(buf, wc, tk && !hist, v, id_of(b, q));
+        if (PEN && __ballot(tk && hist)) {
+          if (nside + __popcll(__ballot(tk && hist)) > kWave) {
+            ovf = true;  // more than 64 history ids of one wave above the threshold: row solver
+          } else {
+            append(side, nside, tk && hist, v, id_of(b, q));
+          }
+        }
+      }
+      return;
+    }
+    // a batch that may not fit: one element slot at a time (picked by selects, so that
+    // the buffer cut below exists once), the buffer cut to its k best when needed
+#pragma unroll 1
+    for (int q = 0; q < NQ; ++q) {
+      float x = 0.0f;
+      uint32_t mw = 0u;
+      bool tk = false;
+#pragma unroll
+      for (int qq = 0; qq < NQ; ++qq) {
+        if (qq == q) {
+          x = unpack_unit<DT>(bt.w[qq / VEC], qq % VEC);
+          mw = MASK ? bt.mw[qq / VEC] : 0u;
+          tk = (bal[qq] >> lane) & 1ull;
+        }
+      }
+      if (!__ballot(tk)) continue;
+      float v = -INFINITY;
+      if (tk) {
+        v = candidate(b, q, x, mw);
+        tk = v >= thr;
+      }
+      const bool hist = hist_inline && tk && in_history(b, q);
+      if (wc + __popcll(__ballot(tk && !hist)) > kTopkWaveCap) {
+        if (wc > k) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
+        tk = tk && v >= thr;
+        if (wc + __popcll(__ballot(tk && !hist)) > kTopkWaveCap) {
+          ovf = true;  // unreachable for k <= 64: the row would go to the row solver
+          return;
+        }
+      }
+      append(buf, wc, tk && !hist, v, id_of(b, q));
+      if (PEN && __ballot(tk && hist)) {
+        if (nside + __popcll(__ballot(tk && hist)) > kWave)
+          ovf = true;
+        else
+          append(side, nside, tk && hist, v, id_of(b, q));
       }
     }
   };
@@ -625,60 +679,143 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
     ib = grab();
     load(ib, bb);
   }
-  if (lane == 0) s.cnt[wave] = wc;
   if (__ballot(bad) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
   if (__ballot(ovf) && lane == 0) atomicOr(&s.flags, kFlagOverflow);
-  __syncthreads();
 
-  // ---- C. union of the wave buffers and the history candidates >= t0; exact top-k ----
-  if (t == 0) {
-    int o = 0;
-    for (int w = 0; w < kWaves; ++w) {
-      s.off[w] = o;
-      o += s.cnt[w];
+  // ---- C. history candidates scored at set-up, the k best of every wave, tree of merges ----
+  const int n_hc = own_hist ? s.n_hc : 0;
+  for (int i0 = wave * kWave; i0 < n_hc; i0 += kBlock) {
+    const uint64_t c = i0 + lane < n_hc ? L.hc[i0 + lane] : 0ull;
+    bool tk = c != 0ull && composite_z(c) >= thr;
+    uint64_t bal = __ballot(tk);
+    if (wc + __popcll(bal) > kTopkWaveCap) {
+      if (wc > k) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
+      tk = tk && composite_z(c) >= thr;
+      bal = __ballot(tk);
     }
-    s.off[kWaves] = o;
-    if (o > kUnionCap) s.flags |= kFlagOverflow;
-    s.n_union = o > kUnionCap ? 0 : o;
+    if (tk) buf[wc + lanes_below(bal)] = c;
+    wc = uniform<int>(wc + __popcll(bal));
+  }
+  if (hist_inline && nside > 0) {  // history ids set aside: penalised now
+    wave_lds_sync();
+    const uint64_t c = lane < nside ? side[lane] : 0ull;
+    float z = -INFINITY;
+    const int id = composite_id(c);
+    if (c != 0ull) z = penalize(composite_z(c), hist_count(L.htab, (uint32_t)a.hash_bits, (uint32_t)id), a.pen);
+    bool tk = z >= thr;
+    uint64_t bal = __ballot(tk);
+    if (wc + __popcll(bal) > kTopkWaveCap) {
+      if (wc > k) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
+      tk = z >= thr;
+      bal = __ballot(tk);
+    }
+    if (tk) buf[wc + lanes_below(bal)] = composite(z, id);
+    wc = uniform<int>(wc + __popcll(bal));
+  }
+  // Final selection: the bin (20 bits of the order key, two levels) that holds the chunk's
+  // k-th best; everything at or above its lower edge is gathered. When that is at most
+  // 64 entries (no wide tie at the edge) one sort finishes the chunk; otherwise every
+  // wave keeps its k best and a tree of bitonic merges combines the waves.
+  if (t == 0) s.n_sel = 0;
+  wave_lds_sync();
+  constexpr int RB = kTopkWaveCap / kWave;
+  uint64_t cv[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    cv[r] = r * kWave + lane < wc ? buf[r * kWave + lane] : 0ull;
+    if (cv[r] != 0ull) key_hist_add(L.kh[2], (uint32_t)(cv[r] >> (64 - kBinBits)));
   }
   __syncthreads();
-  const int n_hc = own_hist ? s.n_top : 0;
-  if (!(s.flags & kFlagOverflow)) {
-    for (int i = lane; i < s.cnt[wave]; i += kWave) L.uni[s.off[wave] + i] = buf[i];
-    for (int i = t; i < n_hc; i += kBlock) {
-      const uint64_t c = L.hc[i];
-      if (composite_z(c) >= t0) {
-        const int pos = atomicAdd(&s.n_union, 1);
-        if (pos < kUnionCap)
-          L.uni[pos] = c;
-        else
-          atomicOr(&s.flags, kFlagOverflow);
-      }
+  const uint32_t total = wave_sum(L.kh[2].coarse[lane]);
+  const uint32_t need = (uint32_t)k < total ? (uint32_t)k : total;
+  uint64_t edge = 0ull;
+  if (need > 0u) {
+    uint32_t fa1, fa2;
+    const int fb1 = key_hist_kth(L.kh[2], need, &fa1);
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      if (cv[r] != 0ull && (int)(cv[r] >> (64 - kBinBits)) == fb1)
+        key_hist_add(L.kh[3], (uint32_t)(cv[r] >> (64 - 2 * kBinBits)) & (kBins - 1));
+    __syncthreads();
+    const int fb2 = key_hist_kth(L.kh[3], need - fa1, &fa2);
+    edge = ((uint64_t)fb1 << (64 - kBinBits)) | ((uint64_t)fb2 << (64 - 2 * kBinBits));
+  } else {
+    __syncthreads();
+  }
+  {
+    int ns = 0;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) ns += __popcll(__ballot(cv[r] != 0ull && cv[r] >= edge));
+    int base = 0;
+    if (lane == 0 && ns > 0) base = atomicAdd(&s.n_sel, ns);
+    base = lane_get(base, 0);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const bool in = cv[r] != 0ull && cv[r] >= edge;
+      const uint64_t m = __ballot(in);
+      const int pos = base + lanes_below(m);
+      if (in && pos < kWave) L.sel[pos] = cv[r];
+      base += __popcll(m);
     }
   }
   __syncthreads();
-  const uint32_t flags = s.flags;
-  if ((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid))) {
+  uint32_t flags = s.flags;
+  const int n_sel = s.n_sel;
+  if (n_sel <= kWave && !((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid)))) {
+    if (wave != 0) return;
+    uint64_t v = lane < n_sel ? L.sel[lane] : 0ull;
+    v = wave_sort64_desc(v);
+    const int n = min(k, n_sel);
     if (INLINE) {
-      solve_row<kBlock, DT>(a, row, L.htab, *reinterpret_cast<SolverShared*>(L.hist));
-    } else if (t == 0) {
+      if (flags & kFlagBadHistory) {
+        if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
+      } else if (flags & kFlagInvalid) {
+        if (lane == 0) a.out_ids[row] = ARBOR_ID_INVALID;
+      } else if (n == 0) {
+        if (lane == 0) a.out_ids[row] = ARBOR_ID_EMPTY;
+      } else {
+        finish_list(a, row, v, n);
+      }
+    } else {
       const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
-      a.hdr[slot * 2 + 0] = 0u;
-      a.hdr[slot * 2 + 1] = flags;
+      if (lane < n) a.cand[slot * kChunkSlot + lane] = v;
+      if (lane == 0) {
+        a.hdr[slot * 2 + 0] = (uint32_t)n;
+        a.hdr[slot * 2 + 1] = flags;
+      }
     }
     return;
   }
-  const int nu = s.n_union;
-  const uint64_t T = block_select_kth<kBlock>(L.uni, nu, k, L.hist, s);
-  if (t == 0) s.n_top = 0;
-  __syncthreads();
-  for (int i = t; i < nu; i += kBlock)
-    if (L.uni[i] >= T) L.wb[atomicAdd(&s.n_top, 1)] = L.uni[i];  // the k best, unordered
-  __syncthreads();
-  if (wave != 0) return;
-  const int n = s.n_top;
-  uint64_t v = lane < n ? L.wb[lane] : 0ull;
+
+  if (wc > kWave) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
+  wave_lds_sync();
+  uint64_t v = lane < wc ? buf[lane] : 0ull;
   v = wave_sort64_desc(v);
+
+  // the list of wave w lives in the first 64 slots of its buffer
+  uint64_t* lists = L.wb;
+#pragma unroll
+  for (int step = 1; step < kWaves; step <<= 1) {
+
+    if ((wave & (2 * step - 1)) == step) lists[wave * kTopkWaveCap + lane] = v;
+    __syncthreads();
+    if (step == 1) {
+      flags = s.flags;
+      if ((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid))) {
+        if (INLINE) {
+          solve_row<kBlock, DT>(a, row, L.htab, *reinterpret_cast<SolverShared*>(L.hist));
+        } else if (t == 0) {
+          const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
+          a.hdr[slot * 2 + 0] = 0u;
+          a.hdr[slot * 2 + 1] = flags;
+        }
+        return;
+      }
+    }
+    if ((wave & (2 * step - 1)) == 0) v = list_merge(v, lists[(wave + step) * kTopkWaveCap + lane]);
+  }
+  if (wave != 0) return;
+  const int n = min(k, list_count(v));
   if (INLINE) {
     if (flags & kFlagBadHistory) {
       if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
@@ -912,7 +1049,8 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.chunk_len = len;
     pl.inline_fin = S == 1;
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
-    pl.lds_stream = pl.mode_k ? arbor::TopkLds::bytes(pl.bitmap_words, p->hist_len, p->hist_len > 0 ? (1 << hb) : 0)
+    const bool mono = p->repetition_penalty >= 1.0f && p->frequency_penalty >= 0.0f && p->presence_penalty >= 0.0f;
+    pl.lds_stream = pl.mode_k ? arbor::TopkLds::bytes(pl.bitmap_words, mono ? 0 : p->hist_len, p->hist_len > 0 ? (1 << hb) : 0)
                               : arbor::lds_total(pl.bitmap_words);
     pl.lds_finish = arbor::lds_total(0);
   }
@@ -1051,6 +1189,7 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   a.out_ids = out_ids;
   a.out_probs = out_probs;
   a.inv_t = 1.0f / p->temperature;
+  a.temp = p->temperature;
   a.pen.rp = p->repetition_penalty;
   a.pen.inv_rp = 1.0f / p->repetition_penalty;
   a.pen.fp = p->frequency_penalty;
@@ -1066,6 +1205,7 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   const size_t esz = p->dtype == ARBOR_DTYPE_BF16 ? 2 : 4;
   a.aligned = ((uintptr_t)logits % 16 == 0) && (((size_t)p->ld_logits * esz) % 16 == 0);
   a.write_probs = probs ? 1 : 0;
+  a.pen_mono = p->repetition_penalty >= 1.0f && p->frequency_penalty >= 0.0f && p->presence_penalty >= 0.0f;
   char* ws = static_cast<char*>(workspace);
   a.hdr = reinterpret_cast<uint32_t*>(ws + pl.off_hdr);
   a.cand = reinterpret_cast<uint64_t*>(ws + pl.off_cand);
