@@ -287,9 +287,6 @@ constexpr int kBins = 1 << kBinBits;
 #ifndef TOPK_UNROLL_F32
 #define TOPK_UNROLL_F32 3
 #endif
-#ifndef TOPK_SAMPLE_BOTH
-#define TOPK_SAMPLE_BOTH 1
-#endif
 
 // Counts of 10-bit key digits with a 64-bin summary (16 bins each), so that the bin of
 // the need-th largest entry is found with two wave scans.
@@ -332,7 +329,6 @@ struct TopkUnroll {
 struct TopkShared {
   int next_batch;
   uint32_t flags;
-  int n_hc;   // penalised history candidates in hc[] (history scored at set-up)
   int n_sel;  // entries at or above the final selection's bin edge
 };
 
@@ -345,23 +341,20 @@ struct TopkLds {
   uint64_t* sel;     // [kWave] the chunk's k best, unordered
   uint64_t* side;    // [kWaves * kWave] history ids whose raw z passed (penalised at the end)
   uint32_t* bitmap;  // [bitmap_words]
-  uint64_t* hc;      // [hist_len] penalised history candidates (history scored at set-up)
   uint32_t* htab;    // [hash_slots]
-  __host__ __device__ static size_t bytes(int bitmap_words, int hist_len, int hash_slots) {
+  __host__ __device__ static size_t bytes(int bitmap_words, int hash_slots) {
     return sizeof(uint64_t) * kWaves * (kTopkWaveCap + kWave) + sizeof(uint32_t) * kWaves * 256 +
-           sizeof(KeyHist) * 4 + sizeof(uint64_t) * kWave + (sizeof(uint32_t) * (size_t)bitmap_words + 7) / 8 * 8 +
-           sizeof(uint64_t) * (size_t)hist_len + sizeof(uint32_t) * (size_t)hash_slots;
+           sizeof(KeyHist) * 4 + sizeof(uint64_t) * kWave + sizeof(uint32_t) * (size_t)bitmap_words +
+           sizeof(uint32_t) * (size_t)hash_slots;
   }
-  __device__ TopkLds(unsigned char* base, int bitmap_words, int hist_len) {
+  __device__ TopkLds(unsigned char* base, int bitmap_words) {
     wb = reinterpret_cast<uint64_t*>(base);
     side = wb + kWaves * kTopkWaveCap;
     hist = reinterpret_cast<uint32_t*>(side + kWaves * kWave);
     kh = reinterpret_cast<KeyHist*>(hist + kWaves * 256);
     sel = reinterpret_cast<uint64_t*>(kh + 4);
     bitmap = reinterpret_cast<uint32_t*>(sel + kWave);
-    hc = reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(bitmap) +
-                                     ((size_t)bitmap_words * sizeof(uint32_t) + 7) / 8 * 8);
-    htab = reinterpret_cast<uint32_t*>(hc + hist_len);
+    htab = bitmap + bitmap_words;
   }
 };
 
@@ -371,7 +364,6 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   constexpr int U = TopkUnroll<DT>::value;
   constexpr int NQ = VEC * U;                       // elements per lane per batch
   constexpr int kBatch = U * kWave;                 // units per batch
-  constexpr int HR = (1 << kMaxHashBits) / kBlock;  // history-table slots per thread
   constexpr int HIDR = (ARBOR_HISTORY_MAX + kBlock - 1) / kBlock;
   static_assert(sizeof(SolverShared) <= sizeof(uint32_t) * kWaves * 256, "solver scratch fits the radix histograms");
   extern __shared__ __align__(16) unsigned char smem[];
@@ -380,7 +372,7 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   // the first chunk of the row
   const bool hist_inline = PEN && a.pen_mono;
   const bool own_hist = PEN && !hist_inline && (blockIdx.x % a.S) == 0;
-  TopkLds L(smem, PEN ? a.bitmap_words : 0, PEN && !a.pen_mono ? a.H : 0);
+  TopkLds L(smem, PEN ? a.bitmap_words : 0);
 
   const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
   const int row = blockIdx.x / a.S, chunk = blockIdx.x % a.S;
@@ -453,7 +445,6 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   if (t == 0) {
     s.next_batch = 2 * kWaves;
     s.flags = 0u;
-    s.n_hc = 0;
   }
   for (int i = t; i < (int)(4 * sizeof(KeyHist) / 4); i += kBlock) reinterpret_cast<uint32_t*>(L.kh)[i] = 0u;
   if (PEN) {
@@ -482,45 +473,19 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
   }
   __syncthreads();
 
-  // ---- the row's distinct history ids, penalised, into hc[] (every thread: HR slots) ----
   bool bad = false;
-  if (own_hist) {
-    const int P = 1 << a.hash_bits;
-    int idq[HR];
-    uint32_t cq[HR], mq[HR];
-    float xq[HR];
-#pragma unroll
-    for (int r = 0; r < HR; ++r) {
-      const int slot = t + r * kBlock;
-      const uint32_t e = slot < P ? L.htab[slot] : kEmptySlot;
-      idq[r] = e != kEmptySlot ? (int)(e >> 12) : -1;
-      cq[r] = (e & 4095u) + 1u;
-      xq[r] = idq[r] >= 0 ? Elem<DT>::one(xrow, idq[r]) : 0.0f;
-      mq[r] = (MASK && idq[r] >= 0) ? mrow[idq[r] >> 5] : ~0u;
-    }
-#pragma unroll
-    for (int r = 0; r < HR; ++r) {
-      if (idq[r] < 0) continue;
-      float z = penalize(xq[r] * a.inv_t + 0.0f, cq[r], a.pen);
-      if (!((mq[r] >> (idq[r] & 31)) & 1u)) z = -INFINITY;
-      if (is_invalid(z)) {
-        bad = true;
-      } else if (z != -INFINITY) {
-        L.hc[atomicAdd(&s.n_hc, 1)] = composite(z, idq[r]);
-      }
-    }
-  }
 
-  // ---- A. threshold from the lane maxima of the first two batches ----
+  // ---- A. threshold T0: a lower bound of the k-th largest of the 1024 lane maxima of
+  // the first two batches (the k-th largest of a subset never exceeds the k-th largest of
+  // the whole): histogram of the order keys' top 10 bits, then of the next 10 bits in the
+  // bin that holds the k-th; every wave reads the bins itself ----
   float t0;
   {
     float lm = -INFINITY;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zsample(ia, ba, q));
-#if TOPK_SAMPLE_BOTH
 #pragma unroll
     for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zsample(ib, bb, q));
-#endif
     const uint32_t key = order_key(lm + 0.0f);
     key_hist_add(L.kh[0], key >> (32 - kBinBits));
     __syncthreads();
@@ -679,22 +644,29 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
     ib = grab();
     load(ib, bb);
   }
-  if (__ballot(bad) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
-  if (__ballot(ovf) && lane == 0) atomicOr(&s.flags, kFlagOverflow);
-
-  // ---- C. history candidates scored at set-up, the k best of every wave, tree of merges ----
-  const int n_hc = own_hist ? s.n_hc : 0;
-  for (int i0 = wave * kWave; i0 < n_hc; i0 += kBlock) {
-    const uint64_t c = i0 + lane < n_hc ? L.hc[i0 + lane] : 0ull;
-    bool tk = c != 0ull && composite_z(c) >= thr;
-    uint64_t bal = __ballot(tk);
-    if (wc + __popcll(bal) > kTopkWaveCap) {
-      if (wc > k) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
-      tk = tk && composite_z(c) >= thr;
-      bal = __ballot(tk);
+  // ---- C. history ids a penalty may raise (the row's first chunk scores all of them),
+  // the history ids set aside while streaming, then the chunk's k best ----
+  if (own_hist) {
+    for (int r = 0; r * kBlock < (1 << a.hash_bits); ++r) {
+      const int slot = t + r * kBlock;
+      const uint32_t e = slot < (1 << a.hash_bits) ? L.htab[slot] : kEmptySlot;
+      const int id = e != kEmptySlot ? (int)(e >> 12) : -1;
+      float z = -INFINITY;
+      if (id >= 0) {
+        z = penalize(Elem<DT>::one(xrow, id) * a.inv_t + 0.0f, (e & 4095u) + 1u, a.pen);
+        if (MASK && !((mrow[id >> 5] >> (id & 31)) & 1u)) z = -INFINITY;
+        if (is_invalid(z)) {
+          bad = true;
+          z = -INFINITY;
+        }
+      }
+      bool tk = z >= thr;
+      if (wc + __popcll(__ballot(tk)) > kTopkWaveCap) {
+        if (wc > k) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
+        tk = z >= thr;
+      }
+      append(buf, wc, tk, z, id);
     }
-    if (tk) buf[wc + lanes_below(bal)] = c;
-    wc = uniform<int>(wc + __popcll(bal));
   }
   if (hist_inline && nside > 0) {  // history ids set aside: penalised now
     wave_lds_sync();
@@ -712,6 +684,9 @@ __global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
     if (tk) buf[wc + lanes_below(bal)] = composite(z, id);
     wc = uniform<int>(wc + __popcll(bal));
   }
+  if (__ballot(bad) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
+  if (__ballot(ovf) && lane == 0) atomicOr(&s.flags, kFlagOverflow);
+
   // Final selection: the bin (20 bits of the order key, two levels) that holds the chunk's
   // k-th best; everything at or above its lower edge is gathered. When that is at most
   // 64 entries (no wide tie at the edge) one sort finishes the chunk; otherwise every
@@ -1049,8 +1024,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.chunk_len = len;
     pl.inline_fin = S == 1;
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
-    const bool mono = p->repetition_penalty >= 1.0f && p->frequency_penalty >= 0.0f && p->presence_penalty >= 0.0f;
-    pl.lds_stream = pl.mode_k ? arbor::TopkLds::bytes(pl.bitmap_words, mono ? 0 : p->hist_len, p->hist_len > 0 ? (1 << hb) : 0)
+    pl.lds_stream = pl.mode_k ? arbor::TopkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0)
                               : arbor::lds_total(pl.bitmap_words);
     pl.lds_finish = arbor::lds_total(0);
   }
