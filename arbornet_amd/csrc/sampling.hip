@@ -25,6 +25,7 @@
 #include <string.h>
 
 #include <cmath>
+#include <mutex>
 
 #include "../../include/arbor_sampling.h"
 #include "args.hpp"
@@ -1040,12 +1041,38 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   return pl;
 }
 
+// Raises a kernel's dynamic LDS limit to at least `lds` bytes. The attribute call costs
+// microseconds of host time, so the limit set for each (kernel, device) is remembered and
+// the call is made only when a launch needs more.
+int allow_lds(const void* kernel, size_t lds) {
+  static std::mutex mu;
+  static const void* fns[512];
+  static int devs[512];
+  static size_t lims[512];
+  static int n = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  std::lock_guard<std::mutex> lock(mu);
+  int slot = -1;
+  for (int i = 0; i < n; ++i)
+    if (fns[i] == kernel && devs[i] == dev) slot = i;
+  if (slot >= 0 && lims[slot] >= lds) return ARBOR_OK;
+  hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute");
+  if (slot < 0 && n < 512) slot = n++;
+  if (slot >= 0) {
+    fns[slot] = kernel;
+    devs[slot] = dev;
+    lims[slot] = lds;
+  }
+  return ARBOR_OK;
+}
+
 template <typename K>
 int launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, const arbor::Args& a) {
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute");
+    const int r = allow_lds(reinterpret_cast<const void*>(kernel), lds);
+    if (r != ARBOR_OK) return r;
   }
   hipLaunchKernelGGL(kernel, grid, block, lds, st, a);
   hipError_t e = hipGetLastError();
