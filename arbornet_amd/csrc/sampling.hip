@@ -33,6 +33,7 @@
 #include "candidates.hpp"
 #include "row_solver.hpp"
 #include "topk_path.hpp"
+#include "topk_stream.hpp"
 
 namespace arbor {
 
@@ -263,555 +264,6 @@ __global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
   }
 }
 
-// ---------------------------------------------------------------------------------------
-// Streaming top-k (1 <= k <= 64): one workgroup per row, or per chunk of a row.
-//
-//  Set-up: the row's history ids are loaded ahead of the logits and fill an LDS bitmap of
-//     the chunk's history ids and an id -> count table while the first two batches of
-//     every wave are in flight.
-//  A. Threshold: T0 is a lower bound of the k-th largest of the 1024 lane maxima of every
-//     wave's first two batches (the k-th largest of a subset never exceeds the k-th
-//     largest of the whole): a histogram of the order keys' top 10 bits, then of the next
-//     10 bits inside the bin that holds the k-th; every wave reads the bins itself.
-//  B. Stream: everything >= the wave's threshold is appended to a per-wave LDS buffer; a
-//     full buffer is cut to its exact k best (wave radix select), raising the threshold.
-//     When no penalty can raise a logit (repetition >= 1, frequency and presence >= 0)
-//     history ids stream past like the others and only those whose raw z passes are
-//     penalised; otherwise they are skipped and scored once at set-up.
-//  C. Finish: each wave sorts its k best (bitonic network over DPP), a tree of bitonic
-//     merges (four barriers) leaves the chunk's k best in wave 0, which draws in fp64 or
-//     publishes them for the row's finish kernel.
-// ---------------------------------------------------------------------------------------
-constexpr int kTopkWaveCap = 256;  // candidates one wave buffers
-constexpr int kBinBits = 10;       // threshold histograms: 2 x 10 bits of the order key
-constexpr int kBins = 1 << kBinBits;
-#ifndef TOPK_UNROLL_F32
-#define TOPK_UNROLL_F32 3
-#endif
-
-// Counts of 10-bit key digits with a 64-bin summary (16 bins each), so that the bin of
-// the need-th largest entry is found with two wave scans.
-struct KeyHist {
-  uint32_t fine[kBins];
-  uint32_t coarse[kBins / 16];
-};
-__device__ __forceinline__ void key_hist_add(KeyHist& h, uint32_t bin) {
-  atomicAdd(&h.fine[bin], 1u);
-  atomicAdd(&h.coarse[bin >> 4], 1u);
-}
-// Bin holding the need-th largest entry (1 <= need <= total), counted from the top bin
-// down; *above = entries in higher bins. Every lane of the wave gets the result.
-__device__ __forceinline__ int key_hist_kth(const KeyHist& h, uint32_t need, uint32_t* above) {
-  static_assert(kBins / 16 == kWave, "one summary bin per lane");
-  const int lane = lane_id();
-  const uint32_t cc = h.coarse[kWave - 1 - lane];  // lane l: l-th highest summary bin
-  const uint32_t ci = wave_scan_incl(cc);
-  const uint64_t hit = __ballot(ci >= need);
-  if (!hit) {
-    *above = lane_get(ci, kWave - 1);
-    return 0;
-  }
-  const int lc = __ffsll((long long)hit) - 1;
-  const uint32_t base = lane_get(ci - cc, lc);
-  const int cbin = kWave - 1 - lc;
-  const uint32_t cf = lane < 16 ? h.fine[cbin * 16 + 15 - lane] : 0u;
-  const uint32_t fi = wave_scan_incl(cf);
-  const int lf = __ffsll((long long)__ballot(lane < 16 && base + fi >= need)) - 1;
-  *above = base + lane_get(fi - cf, lf);
-  return cbin * 16 + 15 - lf;
-}
-
-// 16-byte loads per lane per batch of the streaming top-k kernel (two batches in flight)
-template <int DT>
-struct TopkUnroll {
-  static constexpr int value = DT == ARBOR_DTYPE_F32 ? TOPK_UNROLL_F32 : 2;
-};
-
-struct TopkShared {
-  int next_batch;
-  uint32_t flags;
-  int n_sel;  // entries at or above the final selection's bin edge
-};
-
-// Dynamic LDS of topk_kernel (bytes): wave buffers | radix histograms | threshold
-// histograms | chunk bitmap | history candidates | history table.
-struct TopkLds {
-  uint64_t* wb;      // [kWaves * kTopkWaveCap]; at the end the waves' sorted lists
-  uint32_t* hist;    // [kWaves * 256] wave radix histograms (row solver scratch on fallback)
-  KeyHist* kh;       // [4] threshold sample (two levels), final selection (two levels)
-  uint64_t* sel;     // [kWave] the chunk's k best, unordered
-  uint64_t* side;    // [kWaves * kWave] history ids whose raw z passed (penalised at the end)
-  uint32_t* bitmap;  // [bitmap_words]
-  uint32_t* htab;    // [hash_slots]
-  __host__ __device__ static size_t bytes(int bitmap_words, int hash_slots) {
-    return sizeof(uint64_t) * kWaves * (kTopkWaveCap + kWave) + sizeof(uint32_t) * kWaves * 256 +
-           sizeof(KeyHist) * 4 + sizeof(uint64_t) * kWave + sizeof(uint32_t) * (size_t)bitmap_words +
-           sizeof(uint32_t) * (size_t)hash_slots;
-  }
-  __device__ TopkLds(unsigned char* base, int bitmap_words) {
-    wb = reinterpret_cast<uint64_t*>(base);
-    side = wb + kWaves * kTopkWaveCap;
-    hist = reinterpret_cast<uint32_t*>(side + kWaves * kWave);
-    kh = reinterpret_cast<KeyHist*>(hist + kWaves * 256);
-    sel = reinterpret_cast<uint64_t*>(kh + 4);
-    bitmap = reinterpret_cast<uint32_t*>(sel + kWave);
-    htab = bitmap + bitmap_words;
-  }
-};
-
-template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED>
-__global__ void __launch_bounds__(kBlock) topk_kernel(Args a) {
-  constexpr int VEC = Elem<DT>::kVec;
-  constexpr int U = TopkUnroll<DT>::value;
-  constexpr int NQ = VEC * U;                       // elements per lane per batch
-  constexpr int kBatch = U * kWave;                 // units per batch
-  constexpr int HIDR = (ARBOR_HISTORY_MAX + kBlock - 1) / kBlock;
-  static_assert(sizeof(SolverShared) <= sizeof(uint32_t) * kWaves * 256, "solver scratch fits the radix histograms");
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ TopkShared s;
-  // history ids stream past and are penalised inline, or are scored here at set-up by
-  // the first chunk of the row
-  const bool hist_inline = PEN && a.pen_mono;
-  const bool own_hist = PEN && !hist_inline && (blockIdx.x % a.S) == 0;
-  TopkLds L(smem, PEN ? a.bitmap_words : 0);
-
-  const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
-  const int row = blockIdx.x / a.S, chunk = blockIdx.x % a.S;
-  const int c0 = chunk * a.chunk_len;
-  const int c1 = min(a.V, c0 + a.chunk_len);
-  const void* xrow = row_ptr<DT>(a, row);
-  const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
-  const int n_units = (c1 - c0 + VEC - 1) / VEC;
-  const int n_batches = (n_units + kBatch - 1) / kBatch;
-  const int k = a.top_k;
-
-  // Aligned rows: every lane issues exactly one 16-byte load per unit (a unit past the
-  // chunk reloads the chunk's last unit and is ignored), so the compiler can count the
-  // loads in flight and the next batch overlaps the current one.
-  struct Batch {
-    uint32_t w[U][4];  // raw 16-byte units
-    uint32_t mw[U];
-  };
-  auto load = [&](int bi, Batch& bt) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int unit = bi * kBatch + u * kWave + lane;
-      if (ALIGNED) {
-        const int e0 = c0 + (unit < n_units ? unit : n_units - 1) * VEC;
-        typedef unsigned int u4 __attribute__((ext_vector_type(4)));
-        const u4 v = __builtin_nontemporal_load(
-            reinterpret_cast<const u4*>(static_cast<const char*>(xrow) + (size_t)e0 * Elem<DT>::kBytes));
-        bt.w[u][0] = v.x;
-        bt.w[u][1] = v.y;
-        bt.w[u][2] = v.z;
-        bt.w[u][3] = v.w;
-        if (MASK) bt.mw[u] = mrow[e0 >> 5];
-      } else {
-        const int e0 = c0 + unit * VEC;
-        load_raw<DT>(xrow, e0, c1, false, bt.w[u]);
-        if (MASK) bt.mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
-      }
-    }
-  };
-  // tempered logit of slot q of batch b for the threshold sample: history ids, masked ids,
-  // units past the chunk and NaN / +inf read as -inf (the sample leaves them out)
-  auto zsample = [&](int b, const Batch& bt, int q) -> float {
-    const int u = q / VEC, j = q % VEC;
-    const int unit = b * kBatch + u * kWave + lane;
-    const int e0 = c0 + unit * VEC;
-    if (unit >= n_units) return -INFINITY;
-    float v = unpack_unit<DT>(bt.w[u], j) * a.inv_t;
-    if (PEN && ((L.bitmap[(e0 - c0) >> 5] >> (((e0 - c0) & 31) + j)) & 1u)) v = -INFINITY;
-    if (MASK && !((bt.mw[u] >> ((e0 & 31) + j)) & 1u)) v = -INFINITY;
-    return is_invalid(v) ? -INFINITY : v;
-  };
-
-  // history ids first, so that the set-up waits for them and not for the logits
-  int32_t hid[HIDR];
-  if (PEN) {
-    const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
-#pragma unroll
-    for (int r = 0; r < HIDR; ++r) {
-      const int j = t + r * kBlock;
-      const int32_t v = h[j < a.H ? j : a.H - 1];  // every lane loads: the loads in flight stay countable
-      hid[r] = j < a.H ? v : -1;
-    }
-  }
-  // two batches per wave are in flight while the workgroup sets up
-  Batch ba, bb;
-  int ia = wave, ib = wave + kWaves;
-  load(ia, ba);
-  load(ib, bb);
-
-  if (t == 0) {
-    s.next_batch = 2 * kWaves;
-    s.flags = 0u;
-  }
-  for (int i = t; i < (int)(4 * sizeof(KeyHist) / 4); i += kBlock) reinterpret_cast<uint32_t*>(L.kh)[i] = 0u;
-  if (PEN) {
-    for (int i = t; i < a.bitmap_words; i += kBlock) L.bitmap[i] = 0u;
-    if (own_hist || hist_inline)
-      for (int i = t; i < (1 << a.hash_bits); i += kBlock) L.htab[i] = kEmptySlot;
-  }
-  if (a.write_probs) {
-    float* prow = a.out_probs + (size_t)row * (size_t)a.V;
-    for (int i = c0 + t; i < c1; i += kBlock) prow[i] = 0.0f;
-  }
-  __syncthreads();
-  if (PEN) {
-    bool bad = false;
-#pragma unroll
-    for (int r = 0; r < HIDR; ++r) {
-      const int32_t id = hid[r];
-      if (id >= a.V) {
-        bad = true;
-      } else if (id >= 0) {
-        if (id >= c0 && id < c1) atomicOr(&L.bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
-        if (own_hist || hist_inline) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
-      }
-    }
-    if (bad) atomicOr(&s.flags, kFlagBadHistory);
-  }
-  __syncthreads();
-
-  bool bad = false;
-
-  // ---- A. threshold T0: a lower bound of the k-th largest of the 1024 lane maxima of
-  // the first two batches (the k-th largest of a subset never exceeds the k-th largest of
-  // the whole): histogram of the order keys' top 10 bits, then of the next 10 bits in the
-  // bin that holds the k-th; every wave reads the bins itself ----
-  float t0;
-  {
-    float lm = -INFINITY;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zsample(ia, ba, q));
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zsample(ib, bb, q));
-    const uint32_t key = order_key(lm + 0.0f);
-    key_hist_add(L.kh[0], key >> (32 - kBinBits));
-    __syncthreads();
-    uint32_t above1, above2;
-    const int b1 = key_hist_kth(L.kh[0], (uint32_t)k, &above1);
-    if ((int)(key >> (32 - kBinBits)) == b1) key_hist_add(L.kh[1], (key >> (32 - 2 * kBinBits)) & (kBins - 1));
-    __syncthreads();
-    const int b2 = key_hist_kth(L.kh[1], (uint32_t)k - above1, &above2);
-    // lower edge of the bin: no key in it is smaller; -inf / NaN edges become -FLT_MAX
-    t0 = fmaxf(key_value(((uint32_t)b1 << (32 - kBinBits)) | ((uint32_t)b2 << (32 - 2 * kBinBits))), -FLT_MAX);
-  }
-
-  // ---- B. stream: batches from an LDS counter, two in flight per wave ----
-  uint64_t* buf = L.wb + wave * kTopkWaveCap;
-  uint32_t* rh = L.hist + wave * 256;
-  uint64_t* side = L.side + wave * kWave;
-  int wc = 0, nside = 0;
-  // append z >= thr. The raw test x >= x_thr is implied by z = fl(x * (1/T)) >= thr
-  // (x_thr = thr * T lowered by a relative and an absolute margin), so the hot loop
-  // compares raw logits and computes z only for the few that pass.
-  float thr = 0.0f, x_thr = 0.0f;
-  auto set_thr = [&](float t) {
-    thr = uniform(t);
-    const float tt = thr * a.temp;
-    x_thr = uniform(tt - (fabsf(tt) * 0x1p-20f + 0x1p-120f));
-  };
-  set_thr(t0);
-  bool ovf = false;
-  auto grab = [&]() -> int {
-    int b = 0;
-    if (lane == 0) b = atomicAdd(&s.next_batch, 1);
-    return lane_get(b, 0);
-  };
-  auto id_of = [&](int b, int q) { return c0 + (b * kBatch + (q / VEC) * kWave + lane) * VEC + (q % VEC); };
-  // element q of a batch is past the chunk or masked (mw: its unit's mask word)
-  auto dropped_w = [&](int b, int q, uint32_t mw) -> bool {
-    const int unit = b * kBatch + (q / VEC) * kWave + lane;
-    if (unit >= n_units) return true;
-    return MASK && !((mw >> (((c0 + unit * VEC) & 31) + (q % VEC))) & 1u);
-  };
-  auto in_history = [&](int b, int q) -> bool {
-    const int off = (b * kBatch + (q / VEC) * kWave + lane) * VEC;
-    return PEN && ((L.bitmap[off >> 5] >> ((off & 31) + (q % VEC))) & 1u);
-  };
-  // one candidate (its lane passed the raw test): z, or -inf if not taken (history ids
-  // scored at set-up are not taken here)
-  auto candidate = [&](int b, int q, float x, uint32_t mw) -> float {
-    if (dropped_w(b, q, mw)) return -INFINITY;
-    const float v = x * a.inv_t;
-    if (is_invalid(v)) {
-      bad = true;  // +inf, or overflow to +inf
-      return -INFINITY;
-    }
-    if (PEN && !hist_inline && in_history(b, q)) return -INFINITY;
-    return v;
-  };
-  auto append = [&](uint64_t* dst, int& n, bool tk, float v, int id) {
-    const uint64_t m = __ballot(tk);
-    if (tk) dst[n + lanes_below(m)] = composite(v + 0.0f, id);
-    n = uniform<int>(n + __popcll(m));
-  };
-  auto process = [&](int b, const Batch& bt) {
-    uint64_t bal[NQ];
-    uint64_t any = 0ull, nanm = 0ull;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const float x = unpack_unit<DT>(bt.w[q / VEC], q % VEC);
-      if (MASK) {  // masked ids never pass (most ids of a constrained row are masked)
-        const int e = c0 + (b * kBatch + (q / VEC) * kWave + lane) * VEC;
-        bal[q] = __ballot(x >= x_thr && ((bt.mw[q / VEC] >> ((e & 31) + (q % VEC))) & 1u));
-      } else {
-        bal[q] = __ballot(x >= x_thr);
-      }
-      any |= bal[q];
-      nanm |= __ballot(x != x);
-    }
-    if (nanm) {  // rare: a NaN counts unless masked or past the chunk
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const float x = unpack_unit<DT>(bt.w[q / VEC], q % VEC);
-        if (x != x && !dropped_w(b, q, MASK ? bt.mw[q / VEC] : 0u)) bad = true;
-      }
-    }
-    if (!any) return;
-    int cnt = 0;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) cnt += __popcll(bal[q]);
-    if (wc + cnt <= kTopkWaveCap) {
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        if (!bal[q]) continue;
-        bool tk = (bal[q] >> lane) & 1ull;
-        float v = -INFINITY;
-        if (tk) {
-          v = candidate(b, q, unpack_unit<DT>(bt.w[q / VEC], q % VEC), MASK ? bt.mw[q / VEC] : 0u);
-          tk = v >= thr;
-        }
-        const bool hist = hist_inline && tk && in_history(b, q);  // set aside, penalised at the end
-        append(buf, wc, tk && !hist, v, id_of(b, q));
-        if (PEN && __ballot(tk && hist)) {
-          if (nside + __popcll(__ballot(tk && hist)) > kWave) {
-            ovf = true;  // more than 64 history ids of one wave above the threshold: row solver
-          } else {
-            append(side, nside, tk && hist, v, id_of(b, q));
-          }
-        }
-      }
-      return;
-    }
-    // a batch that may not fit: one element slot at a time (picked by selects, so that
-    // the buffer cut below exists once), the buffer cut to its k best when needed
-#pragma unroll 1
-    for (int q = 0; q < NQ; ++q) {
-      float x = 0.0f;
-      uint32_t mw = 0u;
-      bool tk = false;
-#pragma unroll
-      for (int qq = 0; qq < NQ; ++qq) {
-        if (qq == q) {
-          x = unpack_unit<DT>(bt.w[qq / VEC], qq % VEC);
-          mw = MASK ? bt.mw[qq / VEC] : 0u;
-          tk = (bal[qq] >> lane) & 1ull;
-        }
-      }
-      if (!__ballot(tk)) continue;
-      float v = -INFINITY;
-      if (tk) {
-        v = candidate(b, q, x, mw);
-        tk = v >= thr;
-      }
-      const bool hist = hist_inline && tk && in_history(b, q);
-      if (wc + __popcll(__ballot(tk && !hist)) > kTopkWaveCap) {
-        if (wc > k) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
-        tk = tk && v >= thr;
-        if (wc + __popcll(__ballot(tk && !hist)) > kTopkWaveCap) {
-          ovf = true;  // unreachable for k <= 64: the row would go to the row solver
-          return;
-        }
-      }
-      append(buf, wc, tk && !hist, v, id_of(b, q));
-      if (PEN && __ballot(tk && hist)) {
-        if (nside + __popcll(__ballot(tk && hist)) > kWave)
-          ovf = true;
-        else
-          append(side, nside, tk && hist, v, id_of(b, q));
-      }
-    }
-  };
-  for (;;) {
-    if (ia >= n_batches) break;
-    process(ia, ba);
-    ia = grab();
-    load(ia, ba);
-    if (ib >= n_batches) break;
-    process(ib, bb);
-    ib = grab();
-    load(ib, bb);
-  }
-  // ---- C. history ids a penalty may raise (the row's first chunk scores all of them),
-  // the history ids set aside while streaming, then the chunk's k best ----
-  if (own_hist) {
-    for (int r = 0; r * kBlock < (1 << a.hash_bits); ++r) {
-      const int slot = t + r * kBlock;
-      const uint32_t e = slot < (1 << a.hash_bits) ? L.htab[slot] : kEmptySlot;
-      const int id = e != kEmptySlot ? (int)(e >> 12) : -1;
-      float z = -INFINITY;
-      if (id >= 0) {
-        z = penalize(Elem<DT>::one(xrow, id) * a.inv_t + 0.0f, (e & 4095u) + 1u, a.pen);
-        if (MASK && !((mrow[id >> 5] >> (id & 31)) & 1u)) z = -INFINITY;
-        if (is_invalid(z)) {
-          bad = true;
-          z = -INFINITY;
-        }
-      }
-      bool tk = z >= thr;
-      if (wc + __popcll(__ballot(tk)) > kTopkWaveCap) {
-        if (wc > k) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
-        tk = z >= thr;
-      }
-      append(buf, wc, tk, z, id);
-    }
-  }
-  if (hist_inline && nside > 0) {  // history ids set aside: penalised now
-    wave_lds_sync();
-    const uint64_t c = lane < nside ? side[lane] : 0ull;
-    float z = -INFINITY;
-    const int id = composite_id(c);
-    if (c != 0ull) z = penalize(composite_z(c), hist_count(L.htab, (uint32_t)a.hash_bits, (uint32_t)id), a.pen);
-    bool tk = z >= thr;
-    uint64_t bal = __ballot(tk);
-    if (wc + __popcll(bal) > kTopkWaveCap) {
-      if (wc > k) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
-      tk = z >= thr;
-      bal = __ballot(tk);
-    }
-    if (tk) buf[wc + lanes_below(bal)] = composite(z, id);
-    wc = uniform<int>(wc + __popcll(bal));
-  }
-  if (__ballot(bad) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
-  if (__ballot(ovf) && lane == 0) atomicOr(&s.flags, kFlagOverflow);
-
-  // Final selection: the bin (20 bits of the order key, two levels) that holds the chunk's
-  // k-th best; everything at or above its lower edge is gathered. When that is at most
-  // 64 entries (no wide tie at the edge) one sort finishes the chunk; otherwise every
-  // wave keeps its k best and a tree of bitonic merges combines the waves.
-  if (t == 0) s.n_sel = 0;
-  wave_lds_sync();
-  constexpr int RB = kTopkWaveCap / kWave;
-  uint64_t cv[RB];
-#pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    cv[r] = r * kWave + lane < wc ? buf[r * kWave + lane] : 0ull;
-    if (cv[r] != 0ull) key_hist_add(L.kh[2], (uint32_t)(cv[r] >> (64 - kBinBits)));
-  }
-  __syncthreads();
-  const uint32_t total = wave_sum(L.kh[2].coarse[lane]);
-  const uint32_t need = (uint32_t)k < total ? (uint32_t)k : total;
-  uint64_t edge = 0ull;
-  if (need > 0u) {
-    uint32_t fa1, fa2;
-    const int fb1 = key_hist_kth(L.kh[2], need, &fa1);
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-      if (cv[r] != 0ull && (int)(cv[r] >> (64 - kBinBits)) == fb1)
-        key_hist_add(L.kh[3], (uint32_t)(cv[r] >> (64 - 2 * kBinBits)) & (kBins - 1));
-    __syncthreads();
-    const int fb2 = key_hist_kth(L.kh[3], need - fa1, &fa2);
-    edge = ((uint64_t)fb1 << (64 - kBinBits)) | ((uint64_t)fb2 << (64 - 2 * kBinBits));
-  } else {
-    __syncthreads();
-  }
-  {
-    int ns = 0;
-#pragma unroll
-    for (int r = 0; r < RB; ++r) ns += __popcll(__ballot(cv[r] != 0ull && cv[r] >= edge));
-    int base = 0;
-    if (lane == 0 && ns > 0) base = atomicAdd(&s.n_sel, ns);
-    base = lane_get(base, 0);
-#pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const bool in = cv[r] != 0ull && cv[r] >= edge;
-      const uint64_t m = __ballot(in);
-      const int pos = base + lanes_below(m);
-      if (in && pos < kWave) L.sel[pos] = cv[r];
-      base += __popcll(m);
-    }
-  }
-  __syncthreads();
-  uint32_t flags = s.flags;
-  const int n_sel = s.n_sel;
-  if (n_sel <= kWave && !((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid)))) {
-    if (wave != 0) return;
-    uint64_t v = lane < n_sel ? L.sel[lane] : 0ull;
-    v = wave_sort64_desc(v);
-    const int n = min(k, n_sel);
-    if (INLINE) {
-      if (flags & kFlagBadHistory) {
-        if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
-      } else if (flags & kFlagInvalid) {
-        if (lane == 0) a.out_ids[row] = ARBOR_ID_INVALID;
-      } else if (n == 0) {
-        if (lane == 0) a.out_ids[row] = ARBOR_ID_EMPTY;
-      } else {
-        finish_list(a, row, v, n);
-      }
-    } else {
-      const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
-      if (lane < n) a.cand[slot * kChunkSlot + lane] = v;
-      if (lane == 0) {
-        a.hdr[slot * 2 + 0] = (uint32_t)n;
-        a.hdr[slot * 2 + 1] = flags;
-      }
-    }
-    return;
-  }
-
-  if (wc > kWave) set_thr(fmaxf(thr, wave_keep_topk<kTopkWaveCap>(buf, wc, k, rh)));
-  wave_lds_sync();
-  uint64_t v = lane < wc ? buf[lane] : 0ull;
-  v = wave_sort64_desc(v);
-
-  // the list of wave w lives in the first 64 slots of its buffer
-  uint64_t* lists = L.wb;
-#pragma unroll
-  for (int step = 1; step < kWaves; step <<= 1) {
-
-    if ((wave & (2 * step - 1)) == step) lists[wave * kTopkWaveCap + lane] = v;
-    __syncthreads();
-    if (step == 1) {
-      flags = s.flags;
-      if ((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid))) {
-        if (INLINE) {
-          solve_row<kBlock, DT>(a, row, L.htab, *reinterpret_cast<SolverShared*>(L.hist));
-        } else if (t == 0) {
-          const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
-          a.hdr[slot * 2 + 0] = 0u;
-          a.hdr[slot * 2 + 1] = flags;
-        }
-        return;
-      }
-    }
-    if ((wave & (2 * step - 1)) == 0) v = list_merge(v, lists[(wave + step) * kTopkWaveCap + lane]);
-  }
-  if (wave != 0) return;
-  const int n = min(k, list_count(v));
-  if (INLINE) {
-    if (flags & kFlagBadHistory) {
-      if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
-    } else if (flags & kFlagInvalid) {
-      if (lane == 0) a.out_ids[row] = ARBOR_ID_INVALID;
-    } else if (n == 0) {
-      if (lane == 0) a.out_ids[row] = ARBOR_ID_EMPTY;
-    } else {
-      finish_list(a, row, v, n);
-    }
-  } else {
-    const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
-    if (lane < n) a.cand[slot * kChunkSlot + lane] = v;
-    if (lane == 0) {
-      a.hdr[slot * 2 + 0] = (uint32_t)n;
-      a.hdr[slot * 2 + 1] = flags;
-    }
-  }
-}
-
 // Finishes top-k rows that were split into chunks: wave 0 of a workgroup per row merges
 // the chunks' lists and draws; a row with an overflowed chunk is solved exactly.
 template <int DT>
@@ -1007,14 +459,15 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   pl.hash_bits = hb;
   pl.S = 1;
   if (pl.path == Path::Stream) {
-    // one 1024-thread workgroup per compute unit: split rows only when the batch is
-    // smaller than the chip, and never below 8K ids per chunk
+    // one workgroup per compute unit: split rows only when the batch is smaller than the
+    // chip, and never below 8K ids per chunk
     int S = B < cus ? cus / B : 1;
     const int by_len = (V + 8191) / 8192;
     if (S > by_len) S = by_len;
-    const int slots = pl.mode_k ? arbor::kWaves * arbor::kWaveCap / 2 / pl.k
-                                : arbor::kWaves * arbor::kWaveCap / 2 / arbor::kChunkSlot;
-    if (S > slots) S = slots;
+    if (!pl.mode_k) {  // the min-p finish gathers every chunk's list in LDS
+      const int slots = arbor::kWaves * arbor::kWaveCap / 2 / arbor::kChunkSlot;
+      if (S > slots) S = slots;
+    }
     if (S > arbor::kMaxChunks) S = arbor::kMaxChunks;
     const int by_bitmap = (V + arbor::kMaxChunkLen - 1) / arbor::kMaxChunkLen;
     if (S < by_bitmap) S = by_bitmap;
@@ -1025,7 +478,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.chunk_len = len;
     pl.inline_fin = S == 1;
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
-    pl.lds_stream = pl.mode_k ? arbor::TopkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0)
+    pl.lds_stream = pl.mode_k ? arbor::TkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0)
                               : arbor::lds_total(pl.bitmap_words);
     pl.lds_finish = arbor::lds_total(0);
   }
@@ -1096,12 +549,12 @@ int launch_stream3(bool mode_k, bool inl, dim3 grid, size_t lds, hipStream_t st,
 
 template <int DT, bool PEN, bool MASK, bool ALIGNED>
 int launch_topk4(const Plan& pl, hipStream_t st, const arbor::Args& a) {
-  const dim3 grid((unsigned)(a.B * pl.S)), block(arbor::kBlock);
+  const dim3 grid((unsigned)(a.B * pl.S)), block(arbor::kTkBlock);
   int r = pl.inline_fin
               ? launch(arbor::topk_kernel<DT, PEN, MASK, true, ALIGNED>, grid, block, pl.lds_stream, st, a)
               : launch(arbor::topk_kernel<DT, PEN, MASK, false, ALIGNED>, grid, block, pl.lds_stream, st, a);
   if (r != ARBOR_OK || pl.inline_fin) return r;
-  return launch(arbor::topk_finish_kernel<DT>, dim3((unsigned)a.B), block, pl.lds_solver, st, a);
+  return launch(arbor::topk_finish_kernel<DT>, dim3((unsigned)a.B), dim3(arbor::kBlock), pl.lds_solver, st, a);
 }
 
 template <int DT, bool PEN, bool MASK>

@@ -79,8 +79,9 @@ __device__ __forceinline__ void list_absorb(uint64_t& best, float& thr, int k, u
 
 // fp64 finish of a row from its sorted candidate list (lane i = i-th best, n >= 1 entries):
 // top-p, then min-p, then the first id (ascending) whose running mass exceeds u * E.
-// One wave; writes out_ids[row] and, if asked, the kept probabilities.
-__device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t best, int n) {
+// One wave; writes out_ids[row] and, if asked, the kept probabilities. u is the row's
+// uniform (loaded early by callers that can).
+__device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t best, int n, float u) {
   const int lane = lane_id();
   const bool in = lane < n;
   const double z0 = (double)composite_z(lane_get(best, 0));
@@ -97,21 +98,29 @@ __device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t bes
     const uint64_t low = __ballot(lane < lp && e < (double)a.min_p);
     if (low) kept = __ffsll((long long)low) - 1;
   }
-  // kept ranks [0, kept): order them by id, running mass in id order
+  // kept ranks [0, kept): order them by id (32-bit keys: marker bit 31 | id << 6 | rank;
+  // ids < 2^20), running mass in id order
   const int32_t id = composite_id(best);
-  uint64_t key = lane < kept ? (((uint64_t)(uint32_t)id << 32) | (uint32_t)lane) : ~0ull;
-  key = ~wave_sort64_desc(~key);  // ascending
-  const int r = (int)(uint32_t)key;
+  uint32_t key = lane < kept ? (0x80000000u | ((uint32_t)id << 6) | (uint32_t)lane) : 0u;
+  key = wave_sort64_desc_u32(key);  // descending: the kept ids in lanes [0, kept), largest id first
+  const int r = (int)(key & 63u);
   const double er = __shfl(e, lane < kept ? r : 0);
   const double w = lane < kept ? er : 0.0;
-  const double cid = wave_scan_incl(w);
-  const double E = lane_get(cid, kept - 1);
-  const double target = (double)a.uniforms[row] * E;
+  // running mass in ascending id order = suffix sums over the descending lanes
+  const double tot_w = wave_sum(w);
+  const double cid = tot_w - wave_scan_incl(w) + w;  // sum over lanes >= this one
+  const double E = tot_w;
+  const double target = (double)u * E;
+  // the ascending-first entry with running mass > target: the largest lane index that
+  // satisfies it (lanes descend by id)
   const uint64_t over = __ballot(lane < kept && cid > target);
-  const int pick = over ? __ffsll((long long)over) - 1 : kept - 1;
-  const int32_t pick_id = (int32_t)(lane_get(key, pick) >> 32);
+  const int pick = over ? 63 - __builtin_clzll(over) : 0;
+  const int32_t pick_id = (int32_t)((lane_get(key, pick) >> 6) & 0xFFFFFu);
   if (lane == 0) a.out_ids[row] = pick_id;
-  if (a.write_probs && lane < kept) a.out_probs[(size_t)row * (size_t)a.V + (key >> 32)] = (float)(er / E);
+  if (a.write_probs && lane < kept) a.out_probs[(size_t)row * (size_t)a.V + ((key >> 6) & 0xFFFFFu)] = (float)(er / E);
+}
+__device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t best, int n) {
+  finish_list(a, row, best, n, a.uniforms[row]);
 }
 
 }  // namespace arbor

@@ -1,0 +1,644 @@
+// topk_stream.hpp -- streaming top-k kernel (1 <= k <= 64): one 1024-thread workgroup per
+// row, or per chunk of a row when the batch is smaller than the chip.
+//
+// Fifteen waves stream the row; the sixteenth, the finisher, keeps the row's best 64
+// candidates sorted in its registers, merges what the streaming waves find as they find
+// it, and publishes the k-th best so far as a threshold for them. When the last streaming
+// wave is done, only the candidates of its last batches remain to merge before the draw,
+// so little of the row's fixed work is left after its last byte arrives.
+//
+//  Set-up: the row's history ids are loaded first, then the first batch of logits of every
+//     streaming wave; the LDS is cleared and one barrier passed. Once the first batch has
+//     been sampled the next two are requested, and the history ids fill an LDS bitmap of
+//     the chunk's history ids and an id -> count table.
+//  A. Threshold: every streaming wave adds the maxima of its lanes over its first batch
+//     to an LDS histogram of 12-bit order-key prefixes and takes the lower edge of
+//     the bin that holds the k-th largest value added so far: the k-th largest of any
+//     subset of the row bounds the row's k-th largest from below. History ids are not
+//     excluded from this sample (their penalty is not known there), so thresholds taken
+//     from it are checked at the end: if the k-th best candidate is at or above the
+//     highest of them that any wave used, it was a lower bound too and nothing in the top
+//     k was skipped; otherwise the row is solved exactly (row_solver.hpp).
+//  B. Stream: raw logits are compared with the raw image of the threshold (x >= thr * T
+//     lowered by a margin is implied by z = x * (1/T) >= thr); the slots that pass are
+//     compacted into a per-wave LDS stage with ballots, then tempered, penalised if they
+//     are history ids, checked against the chunk end and NaN / +inf 64 at a time, and
+//     those at or above the threshold are queued for the finisher (an LDS ring). Every
+//     queued candidate's final z also goes into a second histogram, whose k-th largest
+//     is an exact lower bound of the row's k-th best, read with the sample before each
+//     batch; a wave whose batch yields more than k candidates takes their k-th best as
+//     its threshold too.
+//  C. Finisher: takes queued candidates 64 at a time (one bitonic sort and one bitonic
+//     merge into its list, or single insertions for a few) and publishes the k-th best z,
+//     an exact lower bound of the row's k-th best, which the streaming waves read before
+//     each batch. After the last streaming wave it draws in fp64 (topk_path.hpp), or
+//     publishes the chunk's list for topk_finish_kernel.
+//
+// History ids: when no penalty can raise a logit (repetition >= 1, frequency and presence
+// >= 0) an id's penalised z is at most its raw z, so the raw test is enough and history
+// ids are penalised when they pass it. Otherwise they are dropped from the stream and the
+// row's first chunk scores every history id from the table at the end.
+#pragma once
+
+#include "args.hpp"
+#include "block_ops.hpp"
+#include "candidates.hpp"
+#include "row_solver.hpp"
+#include "topk_path.hpp"
+
+namespace arbor {
+
+constexpr int kTkWaves = 16;
+constexpr int kTkBlock = kTkWaves * kWave;  // 1024 threads
+constexpr int kTkStream = kTkWaves - 1;     // streaming waves; the last wave is the finisher
+constexpr int kTkStage = 128;               // raw candidates of one batch staged per wave
+constexpr int kTkQueue = 1024;              // candidate ring between the streamers and the finisher
+constexpr int kSampleBits = 12;             // threshold histogram: top 12 bits of the order key
+constexpr int kSampleBins = 1 << kSampleBits;
+constexpr int kBufferWord3 = 0x00020000;    // buffer resource word 3 (gfx9 family: 32-bit data format)
+constexpr int kBufferNt = 2;                // buffer load cache policy: non-temporal
+// Queue entries whose history status is not known yet have bit 31 of the id word clear
+// (it is set for every id < 2^31); the finisher penalises them.
+constexpr uint64_t kRawMark = 1ull << 31;
+static_assert((kTkQueue & (kTkQueue - 1)) == 0, "the ring size is a power of two");
+
+// 16-byte loads per lane per batch (three batches per lane in flight or in hand)
+#ifndef TK_UNITS_F32
+#define TK_UNITS_F32 2
+#endif
+template <int DT>
+struct TkUnits {
+  static constexpr int value = DT == ARBOR_DTYPE_F32 ? TK_UNITS_F32 : 2;
+};
+
+// Counts of the sample's lane-maximum keys by their top 12 bits, with a 64-bin summary
+// (64 bins each), so that the bin of the k-th largest is found with two wave scans.
+struct SampleHist {
+  uint32_t fine[kSampleBins];
+  uint32_t coarse[kSampleBins / kWave];
+};
+__device__ __forceinline__ void sample_add(SampleHist& h, uint32_t key) {
+  atomicAdd(&h.fine[key >> (32 - kSampleBits)], 1u);
+  atomicAdd(&h.coarse[key >> (32 - kSampleBits + 6)], 1u);
+}
+// Lower edge (as z) of the bin holding the k-th largest key counted so far, or -FLT_MAX
+// when fewer than k keys have been counted or the edge is at or below -FLT_MAX. The
+// histogram may be read while other waves are still adding to it. Every lane gets it.
+__device__ __forceinline__ float sample_threshold(const SampleHist& h, uint32_t k) {
+  static_assert(kSampleBins / kWave == kWave, "one summary bin per lane");
+  const int lane = lane_id();
+  const uint32_t cc = h.coarse[kWave - 1 - lane];  // lane l: l-th highest summary bin
+  const uint32_t ci = wave_scan_incl(cc);
+  const uint64_t hit = __ballot(ci >= k);
+  if (!hit) return -FLT_MAX;
+  const int lc = __ffsll((long long)hit) - 1;
+  const uint32_t base = lane_get(ci - cc, lc);
+  const int cbin = kWave - 1 - lc;
+  const uint32_t cf = h.fine[cbin * kWave + kWave - 1 - lane];
+  const uint32_t fi = wave_scan_incl(cf);
+  const int lf = __ffsll((long long)__ballot(base + fi >= k)) - 1;
+  const uint32_t bin = (uint32_t)(cbin * kWave + kWave - 1 - lf);
+  return fmaxf(key_value(bin << (32 - kSampleBits)), -FLT_MAX);  // NaN edge (below -inf) -> -FLT_MAX
+}
+
+struct TkShared {
+  uint32_t flags;
+  uint32_t tmax;      // order key of the highest sample threshold any wave used
+  int hready;         // streaming waves whose history ids are in the bitmap and the table
+  int done;           // streaming waves that have queued their last candidate
+  uint32_t q_tail;    // candidate slots reserved in the ring
+  uint32_t q_head;    // candidate slots the finisher has taken
+  uint32_t fin_thr;   // bits of the finisher's k-th best z (-FLT_MAX until it holds k)
+  int verdict;        // 1: the finisher's list is exact; 0: the row is solved exactly
+  uint64_t queue[kTkQueue];
+  SampleHist hist;    // lane maxima of every streaming wave's first batch
+  SampleHist chist;   // final z of every queued candidate
+};
+
+// Dynamic LDS of topk_kernel: staged raw candidates | chunk bitmap | history table;
+// the row solver's scratch overlays the stages on fallback.
+struct TkLds {
+  uint64_t* stage;   // [kTkStream * kTkStage]
+  uint32_t* bitmap;  // [bitmap_words]
+  uint32_t* htab;    // [hash_slots]
+  __host__ __device__ static size_t bytes(int bitmap_words, int hash_slots) {
+    return sizeof(uint64_t) * kTkStream * kTkStage + sizeof(uint32_t) * ((size_t)bitmap_words + (size_t)hash_slots);
+  }
+  __device__ TkLds(unsigned char* base, int bitmap_words) {
+    stage = reinterpret_cast<uint64_t*>(base);
+    bitmap = reinterpret_cast<uint32_t*>(stage + kTkStream * kTkStage);
+    htab = bitmap + bitmap_words;
+  }
+};
+static_assert(sizeof(SolverShared) <= sizeof(uint64_t) * kTkStream * kTkStage, "solver scratch fits the stages");
+
+template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED>
+__global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
+  // Every kernel argument the stream uses is read at entry: a scalar load of the argument
+  // segment issued later would be one more memory round trip while the first batches are
+  // in flight (the compiler otherwise loads them where they are first used).
+  __asm__ volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.hist), "s"(a.H), "s"(a.mask), "s"(a.mask_words),
+                   "s"(a.uniforms), "s"(a.inv_t), "s"(a.temp), "s"(a.top_k), "s"(a.S), "s"(a.chunk_len),
+                   "s"(a.hash_bits), "s"(a.bitmap_words), "s"(a.write_probs), "s"(a.pen_mono), "s"(a.top_p),
+                   "s"(a.min_p), "s"(a.out_ids), "s"(a.out_probs));
+  constexpr int VEC = Elem<DT>::kVec;
+  constexpr int U = TkUnits<DT>::value;
+  constexpr int NQ = VEC * U;        // elements per lane per batch
+  constexpr int kBatch = U * kWave;  // units per batch
+  constexpr int HIDR = ARBOR_HISTORY_MAX / (kTkStream * kWave) + 1;  // history ids per streaming lane
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ TkShared s;
+  const bool hist_inline = PEN && a.pen_mono;
+  const bool own_hist = PEN && !hist_inline && (blockIdx.x % a.S) == 0;
+  TkLds L(smem, PEN ? a.bitmap_words : 0);
+
+  const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
+  const bool finisher = wave == kTkStream;
+  const int row = blockIdx.x / a.S, chunk = blockIdx.x % a.S;
+  const int c0 = chunk * a.chunk_len;
+  const int c1 = min(a.V, c0 + a.chunk_len);
+  const void* xrow = row_ptr<DT>(a, row);
+  const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
+  const int n_units = (c1 - c0 + VEC - 1) / VEC;
+  const int n_batches = (n_units + kBatch - 1) / kBatch;
+  const int k = a.top_k;
+
+  struct Batch {
+    uint32_t w[U][4];  // raw 16-byte units
+    uint32_t mw[U];    // mask word of each unit
+  };
+  // Aligned rows are read with range-checked buffer loads over the chunk: every lane
+  // issues one 16-byte load per unit, and a unit past the chunk reads as zeros without a
+  // memory access (it is ignored), so the loads in flight stay countable and the ones
+  // issued past the end cost no memory round trip.
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(static_cast<const char*>(xrow) + (size_t)c0 * Elem<DT>::kBytes), (short)0,
+      (c1 - c0) * Elem<DT>::kBytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t mrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(MASK ? mrow : nullptr), (short)0,
+                                        MASK ? a.mask_words * 4 : 0, kBufferWord3);
+  auto load = [&](int bi, Batch& bt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int unit = bi * kBatch + u * kWave + lane;
+      if (ALIGNED) {
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, unit * 16, 0, kBufferNt);
+        bt.w[u][0] = v.x;
+        bt.w[u][1] = v.y;
+        bt.w[u][2] = v.z;
+        bt.w[u][3] = v.w;
+        if (MASK) bt.mw[u] = __builtin_amdgcn_raw_buffer_load_b32(mrs, ((c0 + unit * VEC) >> 5) * 4, 0, 0);
+      } else {
+        const int e0 = c0 + unit * VEC;
+        load_raw<DT>(xrow, e0, c1, false, bt.w[u]);
+        if (MASK) bt.mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
+      }
+    }
+  };
+  auto unit_of = [&](int b, int q) { return b * kBatch + (q / VEC) * kWave + lane; };
+  auto id_of = [&](int b, int q) { return c0 + unit_of(b, q) * VEC + (q % VEC); };
+  // element q of a batch is past the chunk or masked (mw: its unit's mask word)
+  auto dropped_w = [&](int b, int q, uint32_t mw) -> bool {
+    const int unit = unit_of(b, q);
+    if (unit >= n_units) return true;
+    if (!ALIGNED && c0 + unit * VEC + (q % VEC) >= c1) return true;
+    return MASK && !((mw >> (((c0 + unit * VEC) & 31) + (q % VEC))) & 1u);
+  };
+  // tempered logit of slot q for the threshold sample: ids past the chunk, masked ids and
+  // NaN / +inf read as -inf
+  auto zsample = [&](int b, const Batch& bt, int q) __attribute__((always_inline)) -> float {
+    if (dropped_w(b, q, MASK ? bt.mw[q / VEC] : 0u)) return -INFINITY;
+    const float v = unpack_unit<DT>(bt.w[q / VEC], q % VEC) * a.inv_t;
+    return is_invalid(v) ? -INFINITY : v;
+  };
+
+  // ---- set-up: the history ids (rows of kTkStream * 64 ids; every streaming lane of
+  // such a row loads, clamped, and validity is tested where they are used), the row's
+  // uniform and the first batch of every streaming wave; the LDS is cleared and one
+  // barrier passed. The first batch is the threshold sample; the next two batches are
+  // requested only once it is taken (waves that issue more loads than the memory queue
+  // holds stall at the issue and would take the sample late), and the history ids go
+  // into the LDS table after that, when they have long arrived ----
+  int32_t hraw[HIDR];
+  if (PEN) {
+    const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
+    const int ts = finisher ? 0 : t;
+#pragma unroll
+    for (int r = 0; r < HIDR; ++r) {
+      hraw[r] = -1;
+      if (r * kTkStream * kWave < a.H) {
+        const int j = ts + r * kTkStream * kWave;
+        hraw[r] = h[j < a.H ? j : a.H - 1];
+      }
+    }
+  }
+  float u_row = 0.0f;
+  if (INLINE) {
+    // a vector load (lane-varying zero offset): a scalar one would be waited for by the
+    // first LDS wait, long before the value is needed
+    int zero;
+    __asm__ volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    u_row = a.uniforms[row + zero];
+  }
+  // every wave issues the first batch (no branch around the loads: the compiler would
+  // wait for them at the join); the finisher's is past the chunk, which the range-checked
+  // loads return as zeros without a memory access
+  Batch ba, bb, bc;
+  int ia = finisher ? n_batches : wave, ib = wave + kTkStream, ic = wave + 2 * kTkStream;
+  load(ia, ba);
+  if (t == 0) {
+    s.flags = 0u;
+    s.tmax = 0u;
+    s.hready = 0;
+    s.done = 0;
+    s.q_tail = 0u;
+    s.q_head = 0u;
+    s.fin_thr = __float_as_uint(-FLT_MAX);
+    s.verdict = 1;
+  }
+  for (int i = t; i < kTkQueue; i += kTkBlock) s.queue[i] = 0ull;
+  for (int i = t; i < (int)(sizeof(s.hist) / 4); i += kTkBlock) {
+    reinterpret_cast<uint32_t*>(&s.hist)[i] = 0u;
+    reinterpret_cast<uint32_t*>(&s.chist)[i] = 0u;
+  }
+  if (PEN) {
+    for (int i = t; i < a.bitmap_words; i += kTkBlock) L.bitmap[i] = 0u;
+    if (own_hist || hist_inline)
+      for (int i = t; i < (1 << a.hash_bits); i += kTkBlock) L.htab[i] = kEmptySlot;
+  }
+  __syncthreads();
+  if (a.write_probs) {
+    float* prow = a.out_probs + (size_t)row * (size_t)a.V;
+    for (int i = c0 + t; i < c1; i += kTkBlock) prow[i] = 0.0f;
+  }
+
+  uint64_t best = 0ull;  // the finisher's list: the chunk's best 64 candidates, lane i = i-th
+  uint32_t flags = 0u;
+  if (finisher) {
+    // ---- C. the finisher ----
+    uint32_t head = 0u;
+    float pub = -FLT_MAX;
+    for (;;) {
+      const uint32_t tail = __atomic_load_n(&s.q_tail, __ATOMIC_RELAXED);
+      if (tail == head) {
+        // every streaming wave reserves its last slots before it counts itself done
+        if (__atomic_load_n(&s.done, __ATOMIC_RELAXED) == kTkStream &&
+            __atomic_load_n(&s.q_tail, __ATOMIC_RELAXED) == head)
+          break;
+        __builtin_amdgcn_s_sleep(1);
+        continue;
+      }
+      const int m = (int)min(tail - head, (uint32_t)kWave);
+      const uint32_t slot = (head + (uint32_t)lane) & (kTkQueue - 1);
+      uint64_t c = 0ull;
+      if (lane < m) {
+        // a reserved slot is written by its streaming wave right after the reservation
+        c = __atomic_load_n(&s.queue[slot], __ATOMIC_RELAXED);
+        while (c == 0ull) {
+          __builtin_amdgcn_s_sleep(1);
+          c = __atomic_load_n(&s.queue[slot], __ATOMIC_RELAXED);
+        }
+        s.queue[slot] = 0ull;
+      }
+      if (PEN && __ballot(lane < m && (c & kRawMark) == 0ull)) {
+        // entries queued before every streaming wave's history ids were in the table
+        if (lane == 0)
+          while (__atomic_load_n(&s.hready, __ATOMIC_RELAXED) < kTkStream) __builtin_amdgcn_s_sleep(1);
+        wave_lds_sync();
+        if (lane < m && (c & kRawMark) == 0ull) {
+          c |= kRawMark;
+          const int id = composite_id(c);
+          const int off = id - c0;
+          if ((L.bitmap[off >> 5] >> (off & 31)) & 1u)
+            c = hist_inline ? composite(penalize(composite_z(c), hist_count(L.htab, (uint32_t)a.hash_bits,
+                                                                            (uint32_t)id), a.pen), id)
+                            : 0ull;
+          if (c != 0ull) sample_add(s.chist, (uint32_t)(c >> 32));
+        }
+      }
+      head += (uint32_t)m;
+      wave_lds_sync();
+      if (lane == 0) __atomic_store_n(&s.q_head, head, __ATOMIC_RELAXED);
+      // entries below the list's k-th cannot enter the top k (the streaming waves see the
+      // k-th late); the rest are inserted one by one when few, else sorted and merged
+      {
+        const uint64_t kth0 = lane_get(best, k - 1);
+        const bool keep = c != 0ull && c > kth0;
+        const uint64_t km = __ballot(keep);
+        const int nk = __popcll(km);
+        if (nk > 0 && nk <= 8) {
+          uint64_t rest = km;
+          while (rest) {
+            const int src = __ffsll((long long)rest) - 1;
+            rest &= rest - 1;
+            best = list_insert(best, lane_get(c, src));
+          }
+        } else if (nk > 8) {
+          best = list_merge(best, wave_sort64_desc(keep ? c : 0ull));
+        }
+      }
+      const uint64_t kth = lane_get(best, k - 1);
+      if (kth != 0ull) {
+        const float kz = composite_z(kth);
+        if (kz > pub) {
+          pub = kz;
+          if (lane == 0) __atomic_store_n(&s.fin_thr, __float_as_uint(kz), __ATOMIC_RELAXED);
+        }
+      }
+    }
+    wave_lds_sync();
+    flags = s.flags;
+    // Every candidate passed every threshold its wave used; thresholds from the sample are
+    // lower bounds of the k-th best unless history ids in the sample made them overshoot.
+    // If the k-th best candidate is at or above the highest of them, nothing in the top k
+    // was skipped. Otherwise the row is solved exactly.
+    const uint32_t tm = s.tmax;
+    if (tm != 0u) {
+      const uint64_t kth = lane_get(best, k - 1);
+      if (kth == 0ull || (uint32_t)(kth >> 32) < tm) flags |= kFlagOverflow;
+    }
+    if ((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid)) && lane == 0) s.verdict = 0;
+  } else {
+    // ---- A. the wave's lane maxima over its first batch join the sample; then the next
+    // two batches are requested ----
+    {
+      float lm = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zsample(ia, ba, q));
+      sample_add(s.hist, order_key(lm + 0.0f));
+      wave_lds_sync();
+    }
+    load(ib, bb);
+    load(ic, bc);
+    if (PEN) {
+      bool badh = false;
+#pragma unroll
+      for (int r = 0; r < HIDR; ++r) {
+        const int32_t id = t + r * kTkStream * kWave < a.H ? hraw[r] : -1;
+        if (id >= a.V) {
+          badh = true;
+        } else if (id >= 0) {
+          if (id >= c0 && id < c1) atomicOr(&L.bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
+          if (own_hist || hist_inline) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
+        }
+      }
+      if (__ballot(badh) && lane == 0) atomicOr(&s.flags, kFlagBadHistory);
+      wave_lds_sync();
+      if (lane == 0) atomicAdd(&s.hready, 1);
+    }
+
+    // ---- B. stream ----
+    uint64_t* stage = L.stage + wave * kTkStage;
+    bool bad = false, hwait = PEN;
+    // z >= thr is accepted; x >= x_thr is implied by z = fl(x * (1/T)) >= thr
+    float thr = 0.0f, x_thr = 0.0f;
+    auto set_thr = [&](float tv) {
+      thr = uniform(tv);
+      const float tt = thr * a.temp;
+      x_thr = uniform(tt - (fabsf(tt) * 0x1p-20f + 0x1p-120f));
+    };
+    // thresholds read from the sample histogram are recorded (checked at the end); those
+    // from the candidate histogram (the k-th best queued so far, to a 12-bit bin edge) and
+    // the finisher's k-th best are exact lower bounds
+    uint32_t tmax_w = 0u;
+    auto refresh = [&]() {
+      const float ts = sample_threshold(s.hist, (uint32_t)k);
+      const float tc = fmaxf(sample_threshold(s.chist, (uint32_t)k),
+                             __uint_as_float(__atomic_load_n(&s.fin_thr, __ATOMIC_RELAXED)));
+      if (ts > thr && ts > tc) tmax_w = order_key(ts);
+      const float tn = fmaxf(ts, tc);
+      if (tn > thr) set_thr(tn);
+    };
+    set_thr(-FLT_MAX);
+    refresh();
+    // batches are interleaved over the streaming waves (wave w takes w, w + 15, ...)
+    int nextb = wave + 3 * kTkStream;
+    auto grab = [&]() -> int {
+      const int b = nextb;
+      nextb += kTkStream;
+      return b;
+    };
+    // queue the lanes' candidates (final z) for the finisher
+    auto emit = [&](bool tk, float v, int id, bool raw = false) {
+      const uint64_t m = __ballot(tk);
+      if (!m) return;
+      uint32_t base = 0u;
+      if (lane == 0) base = atomicAdd(&s.q_tail, (uint32_t)__popcll(m));
+      base = lane_get(base, 0);
+      if (tk) {
+        const uint32_t p = base + (uint32_t)lanes_below(m);
+        // the ring slot is free once the finisher has taken the entry kTkQueue places back
+        uint64_t c = composite(v + 0.0f, id);
+        if (raw)
+          c &= ~kRawMark;  // the finisher penalises it and counts its final z
+        else
+          sample_add(s.chist, (uint32_t)(c >> 32));
+        while (p - __atomic_load_n(&s.q_head, __ATOMIC_RELAXED) >= (uint32_t)kTkQueue) __builtin_amdgcn_s_sleep(1);
+        __atomic_store_n(&s.queue[p & (kTkQueue - 1)], c, __ATOMIC_RELAXED);
+      }
+    };
+    // every streaming wave's history ids are in the bitmap and the table (hwait: not seen
+    // yet). Candidates found before are queued raw for the finisher, so no streaming wave
+    // waits for the others' history ids.
+    auto history_ready = [&]() -> bool {
+      if (hwait && __atomic_load_n(&s.hready, __ATOMIC_RELAXED) >= kTkStream) {
+        wave_lds_sync();
+        hwait = false;
+      }
+      return !hwait;
+    };
+    auto wait_history = [&]() {
+      if (hwait) {
+        if (lane == 0)
+          while (__atomic_load_n(&s.hready, __ATOMIC_RELAXED) < kTkStream) __builtin_amdgcn_s_sleep(1);
+        wave_lds_sync();
+        hwait = false;
+      }
+    };
+    // final z of a candidate whose raw logit passed (id inside the chunk, z not NaN / +inf):
+    // history ids are penalised, or dropped (-inf) when the row's first chunk scores them
+    auto final_z = [&](float v, int id) -> float {
+      if (PEN) {
+        const int off = id - c0;
+        if ((L.bitmap[off >> 5] >> (off & 31)) & 1u)
+          v = hist_inline ? penalize(v, hist_count(L.htab, (uint32_t)a.hash_bits, (uint32_t)id), a.pen) : -INFINITY;
+      }
+      return v;
+    };
+    // raw test of slot q: x >= x_thr, or NaN (flagged when it is looked at)
+    auto passes = [&](int b, const Batch& bt, int q) __attribute__((always_inline)) -> bool {
+      const float x = unpack_unit<DT>(bt.w[q / VEC], q % VEC);
+      bool p = !(x < x_thr);
+      if (MASK) p = p && ((bt.mw[q / VEC] >> (((c0 + unit_of(b, q) * VEC) & 31) + (q % VEC))) & 1u);
+      return p;
+    };
+    // one candidate per lane whose raw logit passed. When more than k of the wave's lanes
+    // hold one at or above the threshold, the k-th largest of them (final z) is a lower
+    // bound of the row's k-th best and becomes the wave's threshold (this bounds what is
+    // queued while the threshold is still far below the row's k-th best).
+    auto consider = [&](bool tk, float x, int id) {
+      const bool known = history_ready();
+      float v = -INFINITY;
+      if (tk) {
+        v = x * a.inv_t;
+        if (is_invalid(v)) {
+          bad = true;  // NaN, +inf, or overflow to +inf
+          tk = false;
+        } else if (known) {
+          v = final_z(v, id);
+        }
+      }
+      tk = tk && v >= thr;
+      if (!known) {  // raw z (a penalty only lowers it here): the finisher settles it
+        emit(tk, v, id, true);
+        return;
+      }
+      if (__popcll(__ballot(tk)) > k) {
+        const uint32_t key = tk ? order_key(v) : 0u;
+        uint32_t pre = 0u;
+#pragma unroll 4
+        for (int bit = 31; bit >= 0; --bit) {
+          const uint32_t cnd = pre | (1u << bit);
+          if (__popcll(__ballot(key >= cnd)) >= k) pre = cnd;
+        }
+        set_thr(fmaxf(thr, key_value(pre)));
+        tk = tk && v >= thr;
+      }
+      emit(tk, v, id);
+    };
+    // Staged raw candidates (x bits << 32 | id), 64 per round across the lanes.
+    auto absorb = [&](int ns) {
+#pragma unroll 1
+      for (int j = 0; j < ns; j += kWave) {
+        const int i = j + lane;
+        const uint64_t e = i < ns ? stage[i] : 0ull;
+        const int id = (int)(uint32_t)e;
+        // ids past the chunk are the zeros read past its end
+        consider(i < ns && id < c1, __uint_as_float((uint32_t)(e >> 32)), id);
+      }
+    };
+    auto process = [&](int b, const Batch& bt) __attribute__((always_inline)) {
+      // stage the passing slots while the stage has room
+      int ns = 0;
+      bool full = false;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const bool p = passes(b, bt, q);
+        const uint64_t m = __ballot(p);
+        if (m) {
+          const int c = __popcll(m);
+          if (ns + c <= kTkStage) {
+            if (p)
+              stage[ns + lanes_below(m)] =
+                  ((uint64_t)__float_as_uint(unpack_unit<DT>(bt.w[q / VEC], q % VEC)) << 32) | (uint32_t)id_of(b, q);
+            ns += c;
+          } else {
+            full = true;
+          }
+        }
+      }
+      if (ns == 0 && !full) return;
+      if (!full) {
+        wave_lds_sync();
+        absorb(ns);
+      } else {
+        // more than the stage holds (a threshold far below the row's k-th best): one slot
+        // at a time, picked by selects so that the candidate code exists once
+#pragma unroll 1
+        for (int q = 0; q < NQ; ++q) {
+          float x = 0.0f;
+          uint32_t mw = 0u;
+          bool p = false;
+#pragma unroll
+          for (int qq = 0; qq < NQ; ++qq) {
+            if (qq == q) {
+              x = unpack_unit<DT>(bt.w[qq / VEC], qq % VEC);
+              mw = MASK ? bt.mw[qq / VEC] : 0u;
+              p = passes(b, bt, qq);
+            }
+          }
+          if (!__ballot(p)) continue;
+          consider(p && !dropped_w(b, q, mw), x, id_of(b, q));
+        }
+      }
+    };
+    for (;;) {
+      if (ia >= n_batches) break;
+      refresh();
+      process(ia, ba);
+      ia = grab();
+      load(ia, ba);
+      if (ib >= n_batches) break;
+      process(ib, bb);
+      ib = grab();
+      load(ib, bb);
+      if (ic >= n_batches) break;
+      process(ic, bc);
+      ic = grab();
+      load(ic, bc);
+    }
+
+    // history ids a penalty may raise: the row's first chunk scores all of them
+    wait_history();
+    if (own_hist) {
+      // streaming waves take interleaved 64-slot slices of the table (a power of two >= 64)
+      for (int sb = wave; sb * kWave < (1 << a.hash_bits); sb += kTkStream) {
+        const int slot = sb * kWave + lane;
+        const uint32_t e = L.htab[slot];
+        const int id = e != kEmptySlot ? (int)(e >> 12) : -1;
+        float z = -INFINITY;
+        if (id >= 0) {
+          z = penalize(Elem<DT>::one(xrow, id) * a.inv_t + 0.0f, (e & 4095u) + 1u, a.pen);
+          if (MASK && !((mrow[id >> 5] >> (id & 31)) & 1u)) z = -INFINITY;
+          if (is_invalid(z)) {
+            bad = true;
+            z = -INFINITY;
+          }
+        }
+        emit(z >= thr, z, id);
+      }
+    }
+    const bool wbad = __ballot(bad) != 0ull;  // bad is per lane
+    wave_lds_sync();                          // this wave's queue entries are written
+    if (lane == 0) {
+      if (wbad) atomicOr(&s.flags, kFlagInvalid);
+      if (tmax_w) atomicMax(&s.tmax, tmax_w);
+    }
+    wave_lds_sync();
+    if (lane == 0) atomicAdd(&s.done, 1);
+  }
+  __syncthreads();
+  if (s.verdict == 0) {
+    if (INLINE) {
+      solve_row<kTkBlock, DT>(a, row, L.htab, *reinterpret_cast<SolverShared*>(L.stage));
+    } else if (finisher && lane == 0) {
+      const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
+      a.hdr[slot * 2 + 0] = 0u;
+      a.hdr[slot * 2 + 1] = flags;
+    }
+    return;
+  }
+  if (!finisher) return;
+  const int n = min(k, list_count(best));
+  if (INLINE) {
+    if (flags & kFlagBadHistory) {
+      if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
+    } else if (flags & kFlagInvalid) {
+      if (lane == 0) a.out_ids[row] = ARBOR_ID_INVALID;
+    } else if (n == 0) {
+      if (lane == 0) a.out_ids[row] = ARBOR_ID_EMPTY;
+    } else {
+      finish_list(a, row, best, n, u_row);
+    }
+  } else {
+    const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
+    if (lane < n) a.cand[slot * kChunkSlot + lane] = best;
+    if (lane == 0) {
+      a.hdr[slot * 2 + 0] = (uint32_t)n;
+      a.hdr[slot * 2 + 1] = flags;
+    }
+  }
+}
+
+}  // namespace arbor
