@@ -44,7 +44,8 @@ struct Args {
   int pen_mono;  // repetition >= 1, frequency >= 0, presence >= 0: a penalty never raises z
   uint32_t* hdr;   // [B*S*2]            count, flags of each chunk list
   uint64_t* cand;  // [B*S*kChunkSlot]   sorted candidate composites of each chunk
-  float* zbuf;     // [B*V]              row solver's tempered logits
+  float* zbuf;     // [B*ldz]            row solver's tempered logits
+  int ldz;         // zbuf row stride: V rounded up to 64 floats (rows 256-byte aligned)
 };
 
 template <int DT>

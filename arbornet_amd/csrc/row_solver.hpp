@@ -131,7 +131,7 @@ template <int BLOCK, int DT>
 __device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab, SolverShared& sh) {
   const int t = threadIdx.x;
   const int V = a.V;
-  float* z = a.zbuf + (size_t)row * (size_t)V;
+  float* z = a.zbuf + (size_t)row * (size_t)a.ldz;
   const void* xrow = row_ptr<DT>(a, row);
   const uint32_t* mrow = a.mask ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
   const int P = 1 << a.hash_bits;

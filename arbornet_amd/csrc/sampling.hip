@@ -31,17 +31,23 @@
 #include "args.hpp"
 #include "block_ops.hpp"
 #include "candidates.hpp"
+#include "mass_solver.hpp"
 #include "row_solver.hpp"
 #include "topk_path.hpp"
 #include "topk_stream.hpp"
 
 namespace arbor {
 
+// Dynamic LDS of solver_kernel: history table | FastShared.
+__host__ __device__ constexpr size_t solver_lds_bytes(int hash_bits) {
+  return ((sizeof(uint32_t) << hash_bits) + 15) / 16 * 16 + sizeof(FastShared);
+}
+
 template <int DT>
 __global__ void __launch_bounds__(kBlock) solver_kernel(Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ SolverShared sh;
-  solve_row<kBlock, DT>(a, blockIdx.x, reinterpret_cast<uint32_t*>(smem), sh);
+  FastShared& sh = *reinterpret_cast<FastShared*>(smem + ((sizeof(uint32_t) << a.hash_bits) + 15) / 16 * 16);
+  solve_row_fast<kBlock, DT>(a, blockIdx.x, reinterpret_cast<uint32_t*>(smem), sh);
 }
 
 template <int DT, bool PEN, bool MASK, bool MODE_K, bool INLINE>
@@ -489,7 +495,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   pl.off_cand = off;
   off = align_up(off + sizeof(uint64_t) * arbor::kChunkSlot * (size_t)B * (size_t)pl.S, 256);
   pl.off_zbuf = off;
-  off = align_up(off + sizeof(float) * (size_t)B * (size_t)V, 256);
+  off = align_up(off + sizeof(float) * (size_t)B * align_up((size_t)V, 64), 256);
   pl.total = off;
   return pl;
 }
@@ -664,13 +670,14 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   a.hdr = reinterpret_cast<uint32_t*>(ws + pl.off_hdr);
   a.cand = reinterpret_cast<uint64_t*>(ws + pl.off_cand);
   a.zbuf = reinterpret_cast<float*>(ws + pl.off_zbuf);
+  a.ldz = (int)align_up((size_t)p->vocab, 64);
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (pl.path == Path::Solver) {
     const dim3 grid(p->batch), block(arbor::kBlock);
-    if (p->dtype == ARBOR_DTYPE_BF16)
-      return launch(arbor::solver_kernel<ARBOR_DTYPE_BF16>, grid, block, pl.lds_solver, s, a);
-    return launch(arbor::solver_kernel<ARBOR_DTYPE_F32>, grid, block, pl.lds_solver, s, a);
+    const size_t lds = arbor::solver_lds_bytes(pl.hash_bits);
+    if (p->dtype == ARBOR_DTYPE_BF16) return launch(arbor::solver_kernel<ARBOR_DTYPE_BF16>, grid, block, lds, s, a);
+    return launch(arbor::solver_kernel<ARBOR_DTYPE_F32>, grid, block, lds, s, a);
   }
   const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
   if (p->dtype == ARBOR_DTYPE_BF16) return launch_stream<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a);
