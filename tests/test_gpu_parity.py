@@ -133,6 +133,21 @@ def test_ties_lowest_id_wins(kw):
         assert np.all(ids < kw["top_k"])
 
 
+@pytest.mark.parametrize("kw", [dict(top_p=0.5), dict(top_k=300), dict(top_k=3000, top_p=0.9)])
+@pytest.mark.parametrize("rounded", [False, True])
+def test_solver_many_ties(kw, rounded):
+    # More tied entries at the cut than the row solver ranks directly (1024): all-equal
+    # rows, and integer-valued logits (thousands of exact ties per value).
+    B, V = 4, 5000
+    if rounded:
+        inp = _random_inputs(B, V, seed=23, ties=True)
+    else:
+        inp = syn.Inputs(np.zeros((B, V), np.float32), None, None, np.array([0.0, 0.3, 0.7, 0.999], np.float32))
+    _announce(f"[solver ties] rounded={rounded} {kw}")
+    ids, probs = run_gpu(_params(B, V, inp, **kw), inp, write_probs=True)
+    compare(_params(B, V, inp, **kw), inp, ids, probs, label=f"solver-ties{kw}{rounded}")
+
+
 def test_sentinels():
     B, V = 6, 3000
     inp = _random_inputs(B, V, H=8, mask_frac=0.5, seed=7)
