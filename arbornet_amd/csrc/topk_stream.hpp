@@ -150,7 +150,14 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   __shared__ TkShared s;
   const bool hist_inline = PEN && a.pen_mono;
   const bool own_hist = PEN && !hist_inline && (blockIdx.x % a.S) == 0;
+  // occurrence counts matter only to a frequency penalty; without one, the bitmap says all
+  const bool counts = a.pen.fp != 0.0f;
+  const bool table = own_hist || (hist_inline && counts);
   TkLds L(smem, PEN ? a.bitmap_words : 0);
+  // occurrences of a history id (one whose bitmap bit is set)
+  auto count_of = [&](int id) -> uint32_t {
+    return counts ? hist_count(L.htab, (uint32_t)a.hash_bits, (uint32_t)id) : 1u;
+  };
 
   const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
   const bool finisher = wave == kTkStream;
@@ -264,7 +271,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   }
   if (PEN) {
     for (int i = t; i < a.bitmap_words; i += kTkBlock) L.bitmap[i] = 0u;
-    if (own_hist || hist_inline)
+    if (table)
       for (int i = t; i < (1 << a.hash_bits); i += kTkBlock) L.htab[i] = kEmptySlot;
   }
   __syncthreads();
@@ -311,9 +318,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
           const int id = composite_id(c);
           const int off = id - c0;
           if ((L.bitmap[off >> 5] >> (off & 31)) & 1u)
-            c = hist_inline ? composite(penalize(composite_z(c), hist_count(L.htab, (uint32_t)a.hash_bits,
-                                                                            (uint32_t)id), a.pen), id)
-                            : 0ull;
+            c = hist_inline ? composite(penalize(composite_z(c), count_of(id), a.pen), id) : 0ull;
           if (c != 0ull) sample_add(s.chist, (uint32_t)(c >> 32));
         }
       }
@@ -380,7 +385,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
           badh = true;
         } else if (id >= 0) {
           if (id >= c0 && id < c1) atomicOr(&L.bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
-          if (own_hist || hist_inline) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
+          if (table) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
         }
       }
       if (__ballot(badh) && lane == 0) atomicOr(&s.flags, kFlagBadHistory);
@@ -462,7 +467,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       if (PEN) {
         const int off = id - c0;
         if ((L.bitmap[off >> 5] >> (off & 31)) & 1u)
-          v = hist_inline ? penalize(v, hist_count(L.htab, (uint32_t)a.hash_bits, (uint32_t)id), a.pen) : -INFINITY;
+          v = hist_inline ? penalize(v, count_of(id), a.pen) : -INFINITY;
       }
       return v;
     };
