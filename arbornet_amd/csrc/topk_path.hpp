@@ -98,26 +98,28 @@ __device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t bes
     const uint64_t low = __ballot(lane < lp && e < (double)a.min_p);
     if (low) kept = __ffsll((long long)low) - 1;
   }
-  // kept ranks [0, kept): order them by id (32-bit keys: marker bit 31 | id << 6 | rank;
-  // ids < 2^20), running mass in id order
+  // all n entries ordered by id (32-bit keys: marker bit 31 | id << 6 | rank; ids < 2^20),
+  // independent of the filters above so that the two chains overlap; a sorted lane holds
+  // a kept entry iff its rank is below `kept`
   const int32_t id = composite_id(best);
-  uint32_t key = lane < kept ? (0x80000000u | ((uint32_t)id << 6) | (uint32_t)lane) : 0u;
-  key = wave_sort64_desc_u32(key);  // descending: the kept ids in lanes [0, kept), largest id first
+  uint32_t key = in ? (0x80000000u | ((uint32_t)id << 6) | (uint32_t)lane) : 0u;
+  key = wave_sort64_desc_u32(key);  // descending: lanes [0, n), largest id first
   const int r = (int)(key & 63u);
-  const double er = __shfl(e, lane < kept ? r : 0);
-  const double w = lane < kept ? er : 0.0;
+  const bool kk = key != 0u && r < kept;
+  const double er = __shfl(e, r);
+  const double w = kk ? er : 0.0;
   // running mass in ascending id order = suffix sums over the descending lanes
   const double tot_w = wave_sum(w);
   const double cid = tot_w - wave_scan_incl(w) + w;  // sum over lanes >= this one
   const double E = tot_w;
   const double target = (double)u * E;
-  // the ascending-first entry with running mass > target: the largest lane index that
-  // satisfies it (lanes descend by id)
-  const uint64_t over = __ballot(lane < kept && cid > target);
-  const int pick = over ? 63 - __builtin_clzll(over) : 0;
+  // the ascending-first kept entry with running mass > target: the largest such lane
+  // (lanes descend by id); none (rounding at u -> 1): the largest kept id, the first kept lane
+  const uint64_t over = __ballot(kk && cid > target);
+  const int pick = over ? 63 - __builtin_clzll(over) : __ffsll((long long)__ballot(kk)) - 1;
   const int32_t pick_id = (int32_t)((lane_get(key, pick) >> 6) & 0xFFFFFu);
   if (lane == 0) a.out_ids[row] = pick_id;
-  if (a.write_probs && lane < kept) a.out_probs[(size_t)row * (size_t)a.V + ((key >> 6) & 0xFFFFFu)] = (float)(er / E);
+  if (a.write_probs && kk) a.out_probs[(size_t)row * (size_t)a.V + ((key >> 6) & 0xFFFFFu)] = (float)(er / E);
 }
 __device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t best, int n) {
   finish_list(a, row, best, n, a.uniforms[row]);

@@ -282,6 +282,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
 
   uint64_t best = 0ull;  // the finisher's list: the chunk's best 64 candidates, lane i = i-th
   uint32_t flags = 0u;
+  bool exact = false;  // the finisher's verdict: the row must be solved exactly
   if (finisher) {
     // ---- C. the finisher ----
     uint32_t head = 0u;
@@ -363,7 +364,8 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       const uint64_t kth = lane_get(best, k - 1);
       if (kth == 0ull || (uint32_t)(kth >> 32) < tm) flags |= kFlagOverflow;
     }
-    if ((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid)) && lane == 0) s.verdict = 0;
+    exact = (flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid));
+    if (exact && lane == 0) s.verdict = 0;
   } else {
     // ---- A. the wave's lane maxima over its first batch join the sample; then the next
     // two batches are requested ----
@@ -613,6 +615,29 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     wave_lds_sync();
     if (lane == 0) atomicAdd(&s.done, 1);
   }
+  // The finisher draws (or publishes the chunk's list) before the closing barrier, which
+  // only the exact solver needs: the streaming waves wait there for the verdict.
+  if (finisher && !exact) {
+    const int n = min(k, list_count(best));
+    if (INLINE) {
+      if (flags & kFlagBadHistory) {
+        if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
+      } else if (flags & kFlagInvalid) {
+        if (lane == 0) a.out_ids[row] = ARBOR_ID_INVALID;
+      } else if (n == 0) {
+        if (lane == 0) a.out_ids[row] = ARBOR_ID_EMPTY;
+      } else {
+        finish_list(a, row, best, n, u_row);
+      }
+    } else {
+      const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
+      if (lane < n) a.cand[slot * kChunkSlot + lane] = best;
+      if (lane == 0) {
+        a.hdr[slot * 2 + 0] = (uint32_t)n;
+        a.hdr[slot * 2 + 1] = flags;
+      }
+    }
+  }
   __syncthreads();
   if (s.verdict == 0) {
     if (INLINE) {
@@ -620,27 +645,6 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     } else if (finisher && lane == 0) {
       const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
       a.hdr[slot * 2 + 0] = 0u;
-      a.hdr[slot * 2 + 1] = flags;
-    }
-    return;
-  }
-  if (!finisher) return;
-  const int n = min(k, list_count(best));
-  if (INLINE) {
-    if (flags & kFlagBadHistory) {
-      if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
-    } else if (flags & kFlagInvalid) {
-      if (lane == 0) a.out_ids[row] = ARBOR_ID_INVALID;
-    } else if (n == 0) {
-      if (lane == 0) a.out_ids[row] = ARBOR_ID_EMPTY;
-    } else {
-      finish_list(a, row, best, n, u_row);
-    }
-  } else {
-    const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
-    if (lane < n) a.cand[slot * kChunkSlot + lane] = best;
-    if (lane == 0) {
-      a.hdr[slot * 2 + 0] = (uint32_t)n;
       a.hdr[slot * 2 + 1] = flags;
     }
   }
