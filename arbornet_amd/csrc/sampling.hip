@@ -289,25 +289,39 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
     solve_row<kBlock, DT>(a, row, reinterpret_cast<uint32_t*>(smem), ssh);
     return;
   }
-  if (threadIdx.x >= kWave) return;
+  // wave 0 merges the chunks' lists; with min-p as the only filter (top_k 0) the merged
+  // 64-entry list must hold the whole band, or the row is solved exactly
+  __shared__ int s_exact;
   uint64_t best = 0ull;
-  for (int cb = 0; cb < a.S; cb += 8) {
-    uint64_t v[8];
+  if (threadIdx.x < kWave) {
+    for (int cb = 0; cb < a.S; cb += 8) {
+      uint64_t v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int c = cb + j;
-      v[j] = 0ull;
-      if (c < a.S) {
-        const size_t slot = (size_t)row * (size_t)a.S + (size_t)c;
-        const int n = (int)a.hdr[slot * 2 + 0];
-        if (lane < n) v[j] = a.cand[slot * kChunkSlot + lane];
+      for (int j = 0; j < 8; ++j) {
+        const int c = cb + j;
+        v[j] = 0ull;
+        if (c < a.S) {
+          const size_t slot = (size_t)row * (size_t)a.S + (size_t)c;
+          const int n = (int)a.hdr[slot * 2 + 0];
+          if (lane < n) v[j] = a.cand[slot * kChunkSlot + lane];
+        }
       }
-    }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (cb + j < a.S) best = list_merge(best, v[j]);
+      for (int j = 0; j < 8; ++j)
+        if (cb + j < a.S) best = list_merge(best, v[j]);
+    }
+    const uint64_t last = lane_get(best, kWave - 1), top = lane_get(best, 0);
+    if (lane == 0)
+      s_exact = a.top_k == 0 && last != 0ull && composite_z(last) >= composite_z(top) + a.ln_min_p_lo &&
+                !(flags & (kFlagBadHistory | kFlagInvalid));
   }
-  const int n = min(a.top_k, list_count(best));
+  __syncthreads();
+  if (s_exact) {
+    solve_row<kBlock, DT>(a, row, reinterpret_cast<uint32_t*>(smem), ssh);
+    return;
+  }
+  if (threadIdx.x >= kWave) return;
+  const int n = min(a.top_k > 0 ? a.top_k : kWave, list_count(best));
   if (flags & kFlagBadHistory) {
     if (lane == 0) a.out_ids[row] = ARBOR_ID_BAD_HISTORY;
   } else if (flags & kFlagInvalid) {
@@ -454,9 +468,9 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   if (pl.k > 0 && pl.k <= arbor::kMaxTopK) {
     pl.path = Path::Stream;
     pl.mode_k = true;
-  } else if (minp_only) {
+  } else if (minp_only) {  // the top-k kernel's 64-entry list holds the min-p band
     pl.path = Path::Stream;
-    pl.mode_k = false;
+    pl.mode_k = true;
   } else {
     pl.path = Path::Solver;
   }

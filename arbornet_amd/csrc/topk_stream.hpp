@@ -168,7 +168,11 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
   const int n_units = (c1 - c0 + VEC - 1) / VEC;
   const int n_batches = (n_units + kBatch - 1) / kBatch;
-  const int k = a.top_k;
+  // min-p as the only filter (top_k 0): the list is the whole 64 entries, and it must hold
+  // every id of the band z >= zmax + ln(min_p); ln_lo is that bound's safety-margined log
+  const bool band = a.top_k == 0;
+  const int k = band ? kWave : a.top_k;
+  const float ln_lo = a.ln_min_p_lo;
 
   struct Batch {
     uint32_t w[U][4];  // raw 16-byte units
@@ -345,8 +349,10 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         }
       }
       const uint64_t kth = lane_get(best, k - 1);
-      if (kth != 0ull) {
-        const float kz = composite_z(kth);
+      if (kth != 0ull || (band && best != 0ull)) {
+        // the k-th best, or (band) the best so far + ln_lo, is a lower bound of what is kept
+        float kz = kth != 0ull ? composite_z(kth) : -FLT_MAX;
+        if (band) kz = fmaxf(kz, composite_z(lane_get(best, 0)) + ln_lo);
         if (kz > pub) {
           pub = kz;
           if (lane == 0) __atomic_store_n(&s.fin_thr, __float_as_uint(kz), __ATOMIC_RELAXED);
@@ -360,7 +366,15 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     // If the k-th best candidate is at or above the highest of them, nothing in the top k
     // was skipped. Otherwise the row is solved exactly.
     const uint32_t tm = s.tmax;
-    if (tm != 0u) {
+    if (band) {
+      // the band's lower edge; a full list whose last entry is still inside it may have
+      // dropped members of the band
+      const uint64_t top = lane_get(best, 0);
+      const float edge = composite_z(top) + ln_lo;
+      if (tm != 0u && (top == 0ull || order_key(edge) < tm)) flags |= kFlagOverflow;
+      const uint64_t last = lane_get(best, kWave - 1);
+      if (last != 0ull && composite_z(last) >= edge) flags |= kFlagOverflow;
+    } else if (tm != 0u) {
       const uint64_t kth = lane_get(best, k - 1);
       if (kth == 0ull || (uint32_t)(kth >> 32) < tm) flags |= kFlagOverflow;
     }
@@ -411,8 +425,11 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     uint32_t tmax_w = 0u;
     auto refresh = [&]() {
       const float ts = sample_threshold(s.hist, (uint32_t)k);
-      const float tc = fmaxf(sample_threshold(s.chist, (uint32_t)k),
-                             __uint_as_float(__atomic_load_n(&s.fin_thr, __ATOMIC_RELAXED)));
+      float tc = fmaxf(sample_threshold(s.chist, (uint32_t)k),
+                       __uint_as_float(__atomic_load_n(&s.fin_thr, __ATOMIC_RELAXED)));
+      // band: the bin edge of the largest final z queued bounds zmax from below (not the
+      // sample's largest, which may be a history id that a penalty lowers)
+      if (band) tc = fmaxf(tc, sample_threshold(s.chist, 1u) + ln_lo);
       if (ts > thr && ts > tc) tmax_w = order_key(ts);
       const float tn = fmaxf(ts, tc);
       if (tn > thr) set_thr(tn);
@@ -501,7 +518,13 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         emit(tk, v, id, true);
         return;
       }
-      if (__popcll(__ballot(tk)) > k) {
+      if (band) {
+        const float vm = wave_max(tk ? v : -FLT_MAX);
+        if (vm + ln_lo > thr) {
+          set_thr(vm + ln_lo);
+          tk = tk && v >= thr;
+        }
+      } else if (__popcll(__ballot(tk)) > k) {
         const uint32_t key = tk ? order_key(v) : 0u;
         uint32_t pre = 0u;
 #pragma unroll 4
