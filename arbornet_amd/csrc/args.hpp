@@ -12,9 +12,7 @@ namespace arbor {
 
 constexpr int kBlock = 1024;               // threads of every sampling workgroup
 constexpr int kWaves = kBlock / kWave;     // 16
-constexpr int kWaveCap = 512;              // candidates a wave holds in LDS while streaming
-constexpr int kFinalCap = 1024;            // candidates a row is finished from
-constexpr int kChunkSlot = 256;            // candidates one chunk of a split row publishes
+constexpr int kChunkSlot = 64;             // candidates one chunk of a split row publishes
 constexpr int kMaxTopK = 64;               // largest top-k of the streaming path
 constexpr int kMaxChunks = 64;             // chunks a row may be split into
 constexpr int kMaxChunkLen = 262144;       // ids per chunk (chunk bitmap <= 32 KB)
@@ -54,7 +52,6 @@ template <>
 struct Elem<ARBOR_DTYPE_F32> {
   static constexpr int kVec = 4;
   static constexpr int kBytes = 4;
-  static constexpr int kUnroll = 3;  // 16-byte loads per lane per batch (double-buffered)
   static __device__ __forceinline__ float one(const void* base, int64_t i) {
     return static_cast<const float*>(base)[i];
   }
@@ -72,7 +69,6 @@ template <>
 struct Elem<ARBOR_DTYPE_BF16> {
   static constexpr int kVec = 8;
   static constexpr int kBytes = 2;
-  static constexpr int kUnroll = 2;  // 16-byte loads per lane per batch (double-buffered)
   static __device__ __forceinline__ float one(const void* base, int64_t i) {
     return bf16_bits_to_float(static_cast<const uint16_t*>(base)[i]);
   }

@@ -3,20 +3,17 @@
 //
 // Two device paths compute the same contract:
 //
-//  * streaming path (top-k <= 64, or min-p as the only filter). One 1024-thread
-//    workgroup per compute unit streams a row (or, when the batch is smaller than the
-//    chip, one chunk of a row) from HBM exactly once with 16-byte loads, 8 loads in
-//    flight per lane. Temperature and the allow-mask are applied in registers; ids that
-//    occur in the row's history are skipped through an LDS bitmap and evaluated exactly
-//    once per row at the end. Each wave keeps a private LDS list of candidates above a
-//    running threshold: the k-th best of the 64 lane maxima of every 2048-element batch
-//    (a lower bound of the k-th best seen so far), tightened by an exact wave radix select
-//    when the list fills. The row is finished from at most 1024 candidates in fp64
-//    (top-k, top-p, min-p, inverse-CDF draw in id order), in the same workgroup when the
-//    row was not split, else by finish_kernel from the chunks' published lists.
+//  * streaming top-k path (top-k <= 64, or min-p as the only filter, whose band the
+//    64-entry list then holds): one 1024-thread workgroup per row (or, when the batch is
+//    smaller than the chip, per chunk of a row) reads the row from HBM exactly once;
+//    fifteen waves stream and queue candidates above a rising threshold, the sixteenth
+//    keeps the best 64 and draws in fp64 (topk_stream.hpp, topk_path.hpp). Chunks of a
+//    split row are merged by topk_finish_kernel.
 //
-//  * row solver (top-p without top-k, plain sampling, top-k > 64, or a streamed row whose
-//    candidate list overflowed): see row_solver.hpp.
+//  * row solver (top-p without top-k, plain sampling, top-k > 64): mass_solver.hpp, with
+//    the radix solver of row_solver.hpp as the fallback for heavily tied rows and for
+//    streamed rows whose candidate list could not hold the answer.
+
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdarg.h>
@@ -30,7 +27,6 @@
 #include "../../include/arbor_sampling.h"
 #include "args.hpp"
 #include "block_ops.hpp"
-#include "candidates.hpp"
 #include "mass_solver.hpp"
 #include "row_solver.hpp"
 #include "topk_path.hpp"
@@ -48,226 +44,6 @@ __global__ void __launch_bounds__(kBlock) solver_kernel(Args a) {
   extern __shared__ __align__(16) unsigned char smem[];
   FastShared& sh = *reinterpret_cast<FastShared*>(smem + ((sizeof(uint32_t) << a.hash_bits) + 15) / 16 * 16);
   solve_row_fast<kBlock, DT>(a, blockIdx.x, reinterpret_cast<uint32_t*>(smem), sh);
-}
-
-template <int DT, bool PEN, bool MASK, bool MODE_K, bool INLINE>
-__global__ void __launch_bounds__(kBlock) stream_kernel(Args a) {
-  constexpr int VEC = Elem<DT>::kVec;
-  constexpr int kUnroll = Elem<DT>::kUnroll;
-  extern __shared__ __align__(16) unsigned char smem[];
-  Lds L(smem);
-  __shared__ FinishShared s;
-  const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
-  const int row = blockIdx.x / a.S, chunk = blockIdx.x % a.S;
-  const int c0 = chunk * a.chunk_len;
-  const int c1 = min(a.V, c0 + a.chunk_len);
-  const void* xrow = row_ptr<DT>(a, row);
-
-  if (t == 0) {
-    s.flags = 0u;
-    s.next_batch = 0;
-  }
-  if (PEN) {
-    for (int i = t; i < a.bitmap_words; i += kBlock) L.bitmap[i] = 0u;
-    __syncthreads();
-    const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
-    for (int j = t; j < a.H; j += kBlock) {
-      const int32_t id = h[j];
-      if (id >= c0 && id < c1) atomicOr(&L.bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
-    }
-  }
-  if (a.write_probs) {
-    float* prow = a.out_probs + (size_t)row * (size_t)a.V;
-    for (int i = c0 + t; i < c1; i += kBlock) prow[i] = 0.0f;
-  }
-  __syncthreads();
-
-  // ---- stream the chunk ----
-  // Double-buffered: the loads of batch i+1 are in flight while batch i is processed.
-  uint64_t* buf = L.wbuf + wave * kWaveCap;
-  uint32_t* rh = L.whist + wave * 256;
-  int wc = 0;
-  float thr = -FLT_MAX;  // accept z >= thr; -inf is never a candidate
-  bool bad = false, ovf = false;
-  const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
-  const bool aligned = a.aligned != 0;
-  const int n_units = (c1 - c0 + VEC - 1) / VEC;
-
-  struct Batch {
-    float z[kUnroll][VEC];
-    uint32_t mw[kUnroll];
-  };
-  auto load = [&](int ub, Batch& bt) {
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int e0 = c0 + (ub + u * kWave + lane) * VEC;
-      load_unit<DT>(xrow, e0, c1, aligned, bt.z[u]);
-      if (MASK) bt.mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
-    }
-  };
-  // returns false when the wave's list overflowed (min-p band only)
-  auto process = [&](int ub, Batch& bt) -> bool {
-    float lmax = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int e0 = c0 + (ub + u * kWave + lane) * VEC;
-      const uint32_t mb = MASK ? bt.mw[u] >> (e0 & 31) : ~0u;
-      const uint32_t pb = PEN && e0 < c1 ? L.bitmap[(e0 - c0) >> 5] >> ((e0 - c0) & 31) : 0u;
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        float v = bt.z[u][j] * a.inv_t;
-        if (PEN && ((pb >> j) & 1u)) v = -INFINITY;  // history id: evaluated at the finish
-        if (MASK && !((mb >> j) & 1u)) v = -INFINITY;
-        const bool iv = is_invalid(v);
-        bad |= iv;
-        v = iv ? -INFINITY : v;
-        lmax = fmaxf(lmax, v);
-        bt.z[u][j] = v;
-      }
-    }
-    // raise the threshold from this batch's lane maxima
-    if (MODE_K) {
-      const uint32_t key = wave_sort64_desc_u32(order_key(lmax));
-      thr = fmaxf(thr, key_value(lane_get(key, a.top_k - 1)));
-    } else {
-      const float m = wave_max(lmax);
-      if (m > -INFINITY) thr = fmaxf(thr, m + a.ln_min_p_lo);
-    }
-    int c = 0;
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) c += bt.z[u][j] >= thr ? 1 : 0;
-    int cnt = wave_sum(c);
-    if (cnt == 0) return true;
-    if (wc + cnt > kWaveCap) {
-      if (MODE_K) {
-        if (wc > a.top_k) thr = fmaxf(thr, wave_keep_topk<kWaveCap>(buf, wc, a.top_k, rh));
-      } else if (wc > 0) {
-        thr = fmaxf(thr, wave_keep_band<kWaveCap>(buf, wc, a.ln_min_p_lo));
-      }
-      c = 0;
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) c += bt.z[u][j] >= thr ? 1 : 0;
-      cnt = wave_sum(c);
-    }
-    if (wc + cnt <= kWaveCap) {
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int e0 = c0 + (ub + u * kWave + lane) * VEC;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-          const bool take = bt.z[u][j] >= thr;
-          const uint64_t bal = __ballot(take);
-          if (bal) {
-            if (take) buf[wc + lanes_below(bal)] = composite(bt.z[u][j] + 0.0f, e0 + j);
-            wc += __popcll(bal);
-          }
-        }
-      }
-      return true;
-    }
-    // a batch larger than the buffer: append 64 at a time, pruning in between
-#pragma unroll 1
-    for (int q = 0; q < kUnroll * VEC; ++q) {
-      float v = -INFINITY;
-#pragma unroll
-      for (int uu = 0; uu < kUnroll; ++uu)
-#pragma unroll
-        for (int jj = 0; jj < VEC; ++jj)
-          if (uu * VEC + jj == q) v = bt.z[uu][jj];
-      const int id = c0 + (ub + (q / VEC) * kWave + lane) * VEC + (q % VEC);
-      if (!__ballot(v >= thr)) continue;
-      if (wc + kWave > kWaveCap) {
-        if (MODE_K)
-          thr = fmaxf(thr, wave_keep_topk<kWaveCap>(buf, wc, a.top_k, rh));
-        else
-          thr = fmaxf(thr, wave_keep_band<kWaveCap>(buf, wc, a.ln_min_p_lo));
-        if (wc + kWave > kWaveCap) return false;
-      }
-      const bool take = v >= thr;
-      const uint64_t bal = __ballot(take);
-      if (take) buf[wc + lanes_below(bal)] = composite(v + 0.0f, id);
-      wc += __popcll(bal);
-    }
-    return true;
-  };
-
-  // batches are handed out from an LDS counter, so faster waves take more of them
-  constexpr int kBatch = kUnroll * kWave;  // units per batch
-  const int n_batches = (n_units + kBatch - 1) / kBatch;
-  auto grab = [&]() -> int {
-    int b = 0;
-    if (lane == 0) b = atomicAdd(&s.next_batch, 1);
-    return lane_get(b, 0);
-  };
-  Batch ba, bb;
-  int bi = grab();
-  if (bi < n_batches) load(bi * kBatch, ba);
-  while (bi < n_batches) {
-    int bn = grab();
-    if (bn < n_batches) load(bn * kBatch, bb);
-    if (!process(bi * kBatch, ba)) {
-      ovf = true;
-      break;
-    }
-    bi = bn;
-    if (bi >= n_batches) break;
-    bn = grab();
-    if (bn < n_batches) load(bn * kBatch, ba);
-    if (!process(bi * kBatch, bb)) {
-      ovf = true;
-      break;
-    }
-    bi = bn;
-  }
-  // final wave list: exact top-k (or the band of the wave's best), sorted best first
-  if (!ovf) {
-    if (MODE_K) {
-      if (wc > a.top_k) wave_keep_topk<kWaveCap>(buf, wc, a.top_k, rh);
-    } else if (wc > 0) {
-      wave_keep_band<kWaveCap>(buf, wc, a.ln_min_p_lo);
-    }
-    wave_sort_desc<kWaveCap>(buf, wc);
-  }
-  if (__ballot(bad) && lane == 0) atomicOr(&s.flags, kFlagInvalid);
-  if (ovf && lane == 0) atomicOr(&s.flags, kFlagOverflow);
-  if (lane == 0) {
-    s.cnt[wave] = ovf ? 0 : wc;
-    s.off[wave] = wave * kWaveCap;
-  }
-  __syncthreads();
-
-  if (INLINE) {
-    finish_row<kBlock, DT, MODE_K>(a, row, L.wbuf, kWaves, s.flags, L, s);
-    return;
-  }
-  // ---- publish this chunk's list for finish_kernel ----
-  gather_prefixes<kBlock, MODE_K>(a, L.wbuf, kWaves, L, s);
-  if (t < kWave) {
-    const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;
-    int n = s.n_uni;
-    uint32_t fl = s.flags | (s.uni_over ? kFlagOverflow : 0u);
-    if (!(fl & kFlagOverflow)) {
-      if (MODE_K) {
-        if (n > a.top_k)
-          wave_keep_topk<kFinalCap>(L.uni, n, a.top_k, reinterpret_cast<uint32_t*>(L.wbuf + kWaves * kWaveCap - 128));
-      } else if (n > kChunkSlot) {
-        fl |= kFlagOverflow;
-      }
-    }
-    if (!(fl & kFlagOverflow)) {
-      wave_sort_desc<kFinalCap>(L.uni, n);
-      uint64_t* dst = a.cand + slot * kChunkSlot;
-      for (int i = lane; i < n; i += kWave) dst[i] = L.uni[i];
-    }
-    if (t == 0) {
-      a.hdr[slot * 2 + 0] = (fl & kFlagOverflow) ? 0u : (uint32_t)n;
-      a.hdr[slot * 2 + 1] = fl;
-    }
-  }
 }
 
 // Finishes top-k rows that were split into chunks: wave 0 of a workgroup per row merges
@@ -333,54 +109,6 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
   }
 }
 
-// Finishes rows that were split into chunks: merges the chunks' lists, adds the history
-// ids and draws. One workgroup per row.
-template <int DT, bool MODE_K>
-__global__ void __launch_bounds__(kBlock) finish_kernel(Args a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  Lds L(smem);
-  __shared__ FinishShared s;
-  const int t = threadIdx.x, row = blockIdx.x;
-  if (t == 0) s.flags = 0u;
-  __syncthreads();
-  if (t < a.S) {
-    const size_t slot = (size_t)row * (size_t)a.S + (size_t)t;
-    s.cnt[t] = (int)a.hdr[slot * 2 + 0];
-    atomicOr(&s.flags, a.hdr[slot * 2 + 1]);
-  }
-  __syncthreads();
-  if (t == 0) {
-    int o = 0;
-    for (int c = 0; c < a.S; ++c) {
-      s.off[c] = o;
-      o += s.cnt[c];
-    }
-    s.ints[0] = o;
-  }
-  __syncthreads();
-  // load every list at once: each thread fetches up to 4 entries before storing any
-  constexpr int R = 4;
-  const int total = s.ints[0];
-  uint64_t v[R];
-  int at[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int f = t + r * kBlock;
-    at[r] = -1;
-    if (f < total) {
-      int c = 0;
-      while (f >= s.off[c] + s.cnt[c]) ++c;
-      v[r] = a.cand[((size_t)row * (size_t)a.S + (size_t)c) * kChunkSlot + (size_t)(f - s.off[c])];
-      at[r] = f;
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    if (at[r] >= 0) L.lists[at[r]] = v[r];
-  __syncthreads();
-  finish_row<kBlock, DT, MODE_K>(a, row, L.lists, a.S, s.flags, L, s);
-}
-
 }  // namespace arbor
 
 // =======================================================================================
@@ -408,12 +136,11 @@ enum class Path { Stream, Solver };
 
 struct Plan {
   Path path;
-  bool mode_k;      // stream path: top-k (else: min-p band)
   bool inline_fin;  // stream path: one chunk per row, finished in the same workgroup
   int k;            // effective top-k (0 = off)
   int S, chunk_len;
   int hash_bits, bitmap_words;
-  size_t lds_stream, lds_finish, lds_solver;
+  size_t lds_stream, lds_solver;
   // workspace layout (byte offsets)
   size_t off_hdr, off_cand, off_zbuf, total;
 };
@@ -464,16 +191,10 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   Plan pl{};
   const int V = p->vocab, B = p->batch;
   pl.k = (p->top_k > 0 && p->top_k < V) ? p->top_k : 0;
+  // the streaming top-k kernel: top-k <= 64, or min-p as the only filter (its 64-entry
+  // list then holds the min-p band); everything else goes to the row solver
   const bool minp_only = pl.k == 0 && p->top_p >= 1.0f && p->min_p > 0.0f;
-  if (pl.k > 0 && pl.k <= arbor::kMaxTopK) {
-    pl.path = Path::Stream;
-    pl.mode_k = true;
-  } else if (minp_only) {  // the top-k kernel's 64-entry list holds the min-p band
-    pl.path = Path::Stream;
-    pl.mode_k = true;
-  } else {
-    pl.path = Path::Solver;
-  }
+  pl.path = (pl.k > 0 && pl.k <= arbor::kMaxTopK) || minp_only ? Path::Stream : Path::Solver;
   int hb = 6;
   while ((1 << hb) < 2 * p->hist_len) ++hb;
   pl.hash_bits = hb;
@@ -484,10 +205,6 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     int S = B < cus ? cus / B : 1;
     const int by_len = (V + 8191) / 8192;
     if (S > by_len) S = by_len;
-    if (!pl.mode_k) {  // the min-p finish gathers every chunk's list in LDS
-      const int slots = arbor::kWaves * arbor::kWaveCap / 2 / arbor::kChunkSlot;
-      if (S > slots) S = slots;
-    }
     if (S > arbor::kMaxChunks) S = arbor::kMaxChunks;
     const int by_bitmap = (V + arbor::kMaxChunkLen - 1) / arbor::kMaxChunkLen;
     if (S < by_bitmap) S = by_bitmap;
@@ -498,9 +215,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.chunk_len = len;
     pl.inline_fin = S == 1;
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
-    pl.lds_stream = pl.mode_k ? arbor::TkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0)
-                              : arbor::lds_total(pl.bitmap_words);
-    pl.lds_finish = arbor::lds_total(0);
+    pl.lds_stream = arbor::TkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0);
   }
   pl.lds_solver = sizeof(uint32_t) * (size_t)(1 << hb);
   size_t off = 0;
@@ -553,28 +268,21 @@ int launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, const ar
   return ARBOR_OK;
 }
 
-template <int DT, bool PEN, bool MASK, bool MODE_K>
-int launch_stream4(bool inl, dim3 grid, size_t lds, hipStream_t st, const arbor::Args& a) {
-  const dim3 block(arbor::kBlock);
-  if (inl) return launch(arbor::stream_kernel<DT, PEN, MASK, MODE_K, true>, grid, block, lds, st, a);
-  return launch(arbor::stream_kernel<DT, PEN, MASK, MODE_K, false>, grid, block, lds, st, a);
-}
-
-// the LDS-buffer streaming kernel serves the min-p band; top-k goes to topk_kernel
-template <int DT, bool PEN, bool MASK>
-int launch_stream3(bool mode_k, bool inl, dim3 grid, size_t lds, hipStream_t st, const arbor::Args& a) {
-  (void)mode_k;
-  return launch_stream4<DT, PEN, MASK, false>(inl, grid, lds, st, a);
-}
-
-template <int DT, bool PEN, bool MASK, bool ALIGNED>
-int launch_topk4(const Plan& pl, hipStream_t st, const arbor::Args& a) {
+template <int DT, bool PEN, bool MASK, bool ALIGNED, bool BAND>
+int launch_topk5(const Plan& pl, hipStream_t st, const arbor::Args& a) {
   const dim3 grid((unsigned)(a.B * pl.S)), block(arbor::kTkBlock);
   int r = pl.inline_fin
-              ? launch(arbor::topk_kernel<DT, PEN, MASK, true, ALIGNED>, grid, block, pl.lds_stream, st, a)
-              : launch(arbor::topk_kernel<DT, PEN, MASK, false, ALIGNED>, grid, block, pl.lds_stream, st, a);
+              ? launch(arbor::topk_kernel<DT, PEN, MASK, true, ALIGNED, BAND>, grid, block, pl.lds_stream, st, a)
+              : launch(arbor::topk_kernel<DT, PEN, MASK, false, ALIGNED, BAND>, grid, block, pl.lds_stream, st, a);
   if (r != ARBOR_OK || pl.inline_fin) return r;
   return launch(arbor::topk_finish_kernel<DT>, dim3((unsigned)a.B), dim3(arbor::kBlock), pl.lds_solver, st, a);
+}
+
+// min-p as the only filter (top_k 0) compiles the band rules in
+template <int DT, bool PEN, bool MASK, bool ALIGNED>
+int launch_topk4(const Plan& pl, hipStream_t st, const arbor::Args& a) {
+  if (pl.k == 0) return launch_topk5<DT, PEN, MASK, ALIGNED, true>(pl, st, a);
+  return launch_topk5<DT, PEN, MASK, ALIGNED, false>(pl, st, a);
 }
 
 template <int DT, bool PEN, bool MASK>
@@ -588,23 +296,6 @@ template <int DT>
 int launch_topk(const Plan& pl, bool pen, bool mask, hipStream_t st, const arbor::Args& a) {
   if (pen) return mask ? launch_topk3<DT, true, true>(pl, st, a) : launch_topk3<DT, true, false>(pl, st, a);
   return mask ? launch_topk3<DT, false, true>(pl, st, a) : launch_topk3<DT, false, false>(pl, st, a);
-}
-
-template <int DT>
-int launch_stream(const Plan& pl, bool pen, bool mask, hipStream_t st, const arbor::Args& a) {
-  if (pl.mode_k) return launch_topk<DT>(pl, pen, mask, st, a);
-  const dim3 grid((unsigned)(a.B * pl.S));
-  int r;
-  if (pen)
-    r = mask ? launch_stream3<DT, true, true>(pl.mode_k, pl.inline_fin, grid, pl.lds_stream, st, a)
-             : launch_stream3<DT, true, false>(pl.mode_k, pl.inline_fin, grid, pl.lds_stream, st, a);
-  else
-    r = mask ? launch_stream3<DT, false, true>(pl.mode_k, pl.inline_fin, grid, pl.lds_stream, st, a)
-             : launch_stream3<DT, false, false>(pl.mode_k, pl.inline_fin, grid, pl.lds_stream, st, a);
-  if (r != ARBOR_OK || pl.inline_fin) return r;
-  const dim3 fgrid((unsigned)a.B), block(arbor::kBlock);
-  if (pl.mode_k) return launch(arbor::finish_kernel<DT, true>, fgrid, block, pl.lds_finish, st, a);
-  return launch(arbor::finish_kernel<DT, false>, fgrid, block, pl.lds_finish, st, a);
 }
 
 }  // namespace
@@ -694,8 +385,8 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
     return launch(arbor::solver_kernel<ARBOR_DTYPE_F32>, grid, block, lds, s, a);
   }
   const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
-  if (p->dtype == ARBOR_DTYPE_BF16) return launch_stream<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a);
-  return launch_stream<ARBOR_DTYPE_F32>(pl, pen, mask, s, a);
+  if (p->dtype == ARBOR_DTYPE_BF16) return launch_topk<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a);
+  return launch_topk<ARBOR_DTYPE_F32>(pl, pen, mask, s, a);
 }
 
 int arbor_device_count(int* count) {

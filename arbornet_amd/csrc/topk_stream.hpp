@@ -42,7 +42,6 @@
 
 #include "args.hpp"
 #include "block_ops.hpp"
-#include "candidates.hpp"
 #include "row_solver.hpp"
 #include "topk_path.hpp"
 
@@ -132,7 +131,7 @@ struct TkLds {
 };
 static_assert(sizeof(SolverShared) <= sizeof(uint64_t) * kTkStream * kTkStage, "solver scratch fits the stages");
 
-template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED>
+template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED, bool BAND>
 __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   // Every kernel argument the stream uses is read at entry: a scalar load of the argument
   // segment issued later would be one more memory round trip while the first batches are
@@ -168,9 +167,10 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
   const int n_units = (c1 - c0 + VEC - 1) / VEC;
   const int n_batches = (n_units + kBatch - 1) / kBatch;
-  // min-p as the only filter (top_k 0): the list is the whole 64 entries, and it must hold
-  // every id of the band z >= zmax + ln(min_p); ln_lo is that bound's safety-margined log
-  const bool band = a.top_k == 0;
+  // BAND: min-p as the only filter (top_k 0); the list is the whole 64 entries, and it
+  // must hold every id of the band z >= zmax + ln(min_p); ln_lo is that bound's
+  // safety-margined log
+  constexpr bool band = BAND;
   const int k = band ? kWave : a.top_k;
   const float ln_lo = a.ln_min_p_lo;
 
@@ -366,7 +366,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     // If the k-th best candidate is at or above the highest of them, nothing in the top k
     // was skipped. Otherwise the row is solved exactly.
     const uint32_t tm = s.tmax;
-    if (band) {
+    if constexpr (band) {
       // the band's lower edge; a full list whose last entry is still inside it may have
       // dropped members of the band
       const uint64_t top = lane_get(best, 0);
@@ -429,7 +429,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
                        __uint_as_float(__atomic_load_n(&s.fin_thr, __ATOMIC_RELAXED)));
       // band: the bin edge of the largest final z queued bounds zmax from below (not the
       // sample's largest, which may be a history id that a penalty lowers)
-      if (band) tc = fmaxf(tc, sample_threshold(s.chist, 1u) + ln_lo);
+      if constexpr (band) tc = fmaxf(tc, sample_threshold(s.chist, 1u) + ln_lo);
       if (ts > thr && ts > tc) tmax_w = order_key(ts);
       const float tn = fmaxf(ts, tc);
       if (tn > thr) set_thr(tn);
@@ -518,7 +518,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         emit(tk, v, id, true);
         return;
       }
-      if (band) {
+      if constexpr (band) {
         const float vm = wave_max(tk ? v : -FLT_MAX);
         if (vm + ln_lo > thr) {
           set_thr(vm + ln_lo);
