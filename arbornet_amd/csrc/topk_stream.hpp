@@ -100,6 +100,18 @@ __device__ __forceinline__ float sample_threshold(const SampleHist& h, uint32_t 
   return fmaxf(key_value(bin << (32 - kSampleBits)), -FLT_MAX);  // NaN edge (below -inf) -> -FLT_MAX
 }
 
+// The k-th largest of the lanes' order keys (0 = none), given at least k nonzero keys:
+// the largest prefix with at least k keys at or above it, found bit by bit with ballots.
+__device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, int k) {
+  uint32_t pre = 0u;
+#pragma unroll 4
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cnd = pre | (1u << bit);
+    if (__popcll(__ballot(key >= cnd)) >= k) pre = cnd;
+  }
+  return pre;
+}
+
 struct TkShared {
   uint32_t flags;
   uint32_t tmax;      // order key of the highest sample threshold any wave used
@@ -525,14 +537,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
           tk = tk && v >= thr;
         }
       } else if (__popcll(__ballot(tk)) > k) {
-        const uint32_t key = tk ? order_key(v) : 0u;
-        uint32_t pre = 0u;
-#pragma unroll 4
-        for (int bit = 31; bit >= 0; --bit) {
-          const uint32_t cnd = pre | (1u << bit);
-          if (__popcll(__ballot(key >= cnd)) >= k) pre = cnd;
-        }
-        set_thr(fmaxf(thr, key_value(pre)));
+        set_thr(fmaxf(thr, key_value(wave_kth_key(tk ? order_key(v) : 0u, k))));
         tk = tk && v >= thr;
       }
       emit(tk, v, id);
@@ -552,24 +557,55 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       // stage the passing slots while the stage has room
       int ns = 0;
       bool full = false;
+      auto stage_passing = [&]() __attribute__((always_inline)) {
+        ns = 0;
+        full = false;
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const bool p = passes(b, bt, q);
-        const uint64_t m = __ballot(p);
-        if (m) {
-          const int c = __popcll(m);
-          if (ns + c <= kTkStage) {
-            if (p)
-              stage[ns + lanes_below(m)] =
-                  ((uint64_t)__float_as_uint(unpack_unit<DT>(bt.w[q / VEC], q % VEC)) << 32) | (uint32_t)id_of(b, q);
-            ns += c;
-          } else {
-            full = true;
+        for (int q = 0; q < NQ; ++q) {
+          const bool p = passes(b, bt, q);
+          const uint64_t m = __ballot(p);
+          if (m) {
+            const int c = __popcll(m);
+            if (ns + c <= kTkStage) {
+              if (p)
+                stage[ns + lanes_below(m)] =
+                    ((uint64_t)__float_as_uint(unpack_unit<DT>(bt.w[q / VEC], q % VEC)) << 32) | (uint32_t)id_of(b, q);
+              ns += c;
+            } else {
+              full = true;
+            }
           }
+        }
+      };
+      stage_passing();
+      if (MASK && __builtin_expect(full, 0)) {
+        // More passing slots than the stage holds (a threshold far below the row's k-th
+        // best, as on masked rows, whose masked lanes leave the sample short): the k-th
+        // largest of the lanes' best passing z, k distinct ids, bounds the row's k-th best
+        // from below (band: the best one bounds zmax). Raw values cannot see penalties, so
+        // with history ids the bound is checked at the end like the sample. Rows without a
+        // mask rarely get here and keep the code of their stream loop small.
+        float lm = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          if (passes(b, bt, q) && !dropped_w(b, q, MASK ? bt.mw[q / VEC] : 0u))
+            lm = fmaxf(lm, unpack_unit<DT>(bt.w[q / VEC], q % VEC));
+        const float zl = lm * a.inv_t + 0.0f;
+        const uint32_t key = lm > -INFINITY && !is_invalid(zl) ? order_key(zl) : 0u;
+        float tb = -FLT_MAX;
+        if (__popcll(__ballot(key != 0u)) >= k) tb = key_value(wave_kth_key(key, k));
+        if constexpr (band) {
+          const uint32_t km = wave_max(key);
+          if (km != 0u) tb = fmaxf(tb, key_value(km) + ln_lo);
+        }
+        if (tb > thr) {
+          if (PEN) tmax_w = max(tmax_w, order_key(tb));
+          set_thr(tb);
+          stage_passing();
         }
       }
       if (ns == 0 && !full) return;
-      if (!full) {
+      if (__builtin_expect(!full, 1)) {
         wave_lds_sync();
         absorb(ns);
       } else {
