@@ -181,6 +181,31 @@ def test_uniform_extremes():
         compare(_params(B, V, inp, **kw), inp, ids, label=f"uext{kw}")
 
 
+@pytest.mark.parametrize("kw", [dict(top_k=8, repetition_penalty=3.0), dict(top_k=30, top_p=0.8, presence_penalty=2.0),
+                                dict(min_p=0.3, frequency_penalty=1.5), dict(top_k=8, repetition_penalty=0.5)])
+def test_masked_block_with_penalised_leaders(kw):
+    # Only a contiguous block of each row is allowed, so the first batches over the block
+    # overflow the stage and raise thresholds from raw values; the block's largest logits
+    # are history ids, which the penalties lower (or, repetition < 1, raise). The kept set
+    # must still be exact (thresholds that overshot send the row to the exact solver).
+    B, V = 8, 40000
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    allowed = np.zeros((B, V), bool)
+    hist = np.full((B, 64), -1, np.int32)
+    for r in range(B):
+        lo = int(rng.integers(0, V - 4096))
+        allowed[r, lo:lo + 4096] = True
+        lead = lo + np.argsort(x[r, lo:lo + 4096])[::-1][:40]
+        x[r, lead[:20]] += 6.0
+        hist[r, :40] = lead
+        hist[r, 40:48] = lead[:8]  # repeats
+    inp = syn.Inputs(x, hist, pack_mask(allowed), rng.random(B).astype(np.float32))
+    _announce(f"[masked leaders] {kw}")
+    ids, probs = run_gpu(_params(B, V, inp, **kw), inp, write_probs=True)
+    compare(_params(B, V, inp, **kw), inp, ids, probs, label=f"masked-leaders{kw}")
+
+
 def test_minp_overflow_falls_back_to_row_solver():
     # flat logits: every token is inside the min-p band, so the stream path's candidate
     # lists overflow and the finishing workgroup solves the row exactly instead
