@@ -104,6 +104,42 @@ __device__ __forceinline__ void fs_visit(const float* z, int V, F f) {
   }
 }
 
+// Tempered, masked logits z[i] = x[i] * (1/T) (or -inf where the mask clears i) for i in
+// [c0, c1), c0 a multiple of 32: VEC-entry units, kFsLoads units in flight per thread.
+// z is the row's padded buffer (16-byte aligned, room up to the next multiple of 64).
+template <int BLOCK, int DT>
+__device__ __forceinline__ void fs_temper(const Args& a, const void* xrow, const uint32_t* mrow, float* z, int c0,
+                                          int c1) {
+  constexpr int VEC = Elem<DT>::kVec;
+  const bool aligned = a.aligned != 0;
+  const int nu = (c1 - c0 + VEC - 1) / VEC;
+  for (int base = threadIdx.x; base < nu; base += BLOCK * kFsLoads) {
+    float x[kFsLoads][VEC];
+#pragma unroll
+    for (int u = 0; u < kFsLoads; ++u) {
+      const int q = base + u * BLOCK;
+      if (q < nu) load_unit<DT>(xrow, c0 + q * VEC, c1, aligned, x[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kFsLoads; ++u) {
+      const int q = base + u * BLOCK;
+      if (q >= nu) continue;
+      const int e0 = c0 + q * VEC;
+      const uint32_t bits = mrow ? mrow[e0 >> 5] >> (e0 & 31) : 0xFFFFFFFFu;
+#pragma unroll
+      for (int c = 0; c < VEC; c += 4) {
+        fs_f4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v = x[u][c + j] * a.inv_t + 0.0f;
+          o[j] = ((bits >> (c + j)) & 1u) ? v : -INFINITY;
+        }
+        if (e0 + c < c1) *reinterpret_cast<fs_f4*>(z + e0 + c) = o;
+      }
+    }
+  }
+}
+
 // Level-0 bin of d = zmax - v (scale = kFsBins / span), and the level-1 sub-bin of an
 // entry of level-0 bin b0. Non-decreasing in d, i.e. bins ascend as the rank descends.
 __device__ __forceinline__ float fs_x(float v, float zmax, float scale) { return (zmax - v) * scale; }
@@ -294,36 +330,8 @@ __device__ void solve_row_fast(const Args& a, int row, uint32_t* htab, FastShare
         hist_insert(htab, (uint32_t)a.hash_bits, (uint32_t)id);
     }
   }
-  // 2. tempered, masked logits: VEC-entry units, kFsLoads units in flight per thread
-  {
-    constexpr int VEC = Elem<DT>::kVec;
-    const bool aligned = a.aligned != 0;
-    const int nu = (V + VEC - 1) / VEC;
-    for (int base = t; base < nu; base += BLOCK * kFsLoads) {
-      float x[kFsLoads][VEC];
-#pragma unroll
-      for (int u = 0; u < kFsLoads; ++u) {
-        const int q = base + u * BLOCK;
-        if (q < nu) load_unit<DT>(xrow, q * VEC, V, aligned, x[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < kFsLoads; ++u) {
-        const int q = base + u * BLOCK;
-        if (q >= nu) continue;
-        const uint32_t bits = mrow ? mrow[(q * VEC) >> 5] >> ((q * VEC) & 31) : 0xFFFFFFFFu;
-#pragma unroll
-        for (int c = 0; c < VEC; c += 4) {
-          fs_f4 o;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float v = x[u][c + j] * a.inv_t + 0.0f;
-            o[j] = ((bits >> (c + j)) & 1u) ? v : -INFINITY;
-          }
-          if (q * VEC + c < V) *reinterpret_cast<fs_f4*>(z + q * VEC + c) = o;
-        }
-      }
-    }
-  }
+  // 2. tempered, masked logits
+  fs_temper<BLOCK, DT>(a, xrow, mrow, z, 0, V);
   __syncthreads();
   // 3. penalties, one writer per distinct history id
   if (a.H > 0) {

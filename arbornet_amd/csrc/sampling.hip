@@ -29,6 +29,7 @@
 #include "block_ops.hpp"
 #include "mass_solver.hpp"
 #include "row_solver.hpp"
+#include "split_solver.hpp"
 #include "topk_path.hpp"
 #include "topk_stream.hpp"
 
@@ -142,7 +143,7 @@ struct Plan {
   int hash_bits, bitmap_words;
   size_t lds_stream, lds_solver;
   // workspace layout (byte offsets)
-  size_t off_hdr, off_cand, off_zbuf, total;
+  size_t off_hdr, off_cand, off_zbuf, off_split, off_ctr, total;
 };
 
 int validate(const arbor_sampling_params* p) {
@@ -216,6 +217,16 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.inline_fin = S == 1;
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
     pl.lds_stream = arbor::TkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0);
+  } else if (B < cus) {
+    // row solver over S workgroups per row (cooperative launch), never below 8K ids per chunk
+    int S = cus / B;
+    const int by_len = (V + 8191) / 8192;
+    if (S > by_len) S = by_len;
+    if (S > 1) {
+      const int len = (int)align_up((size_t)((V + S - 1) / S), 512);
+      pl.S = (V + len - 1) / len;
+      pl.chunk_len = len;
+    }
   }
   pl.lds_solver = sizeof(uint32_t) * (size_t)(1 << hb);
   size_t off = 0;
@@ -225,6 +236,13 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   off = align_up(off + sizeof(uint64_t) * arbor::kChunkSlot * (size_t)B * (size_t)pl.S, 256);
   pl.off_zbuf = off;
   off = align_up(off + sizeof(float) * (size_t)B * align_up((size_t)V, 64), 256);
+  pl.off_split = off;
+  pl.off_ctr = off;
+  if (pl.path == Path::Solver && pl.S > 1) {
+    off = align_up(off + sizeof(arbor::SplitChunk) * (size_t)B * (size_t)pl.S, 256);
+    pl.off_ctr = off;
+    off = align_up(off + sizeof(uint32_t) * (size_t)B, 256);
+  }
   pl.total = off;
   return pl;
 }
@@ -296,6 +314,61 @@ template <int DT>
 int launch_topk(const Plan& pl, bool pen, bool mask, hipStream_t st, const arbor::Args& a) {
   if (pen) return mask ? launch_topk3<DT, true, true>(pl, st, a) : launch_topk3<DT, true, false>(pl, st, a);
   return mask ? launch_topk3<DT, false, true>(pl, st, a) : launch_topk3<DT, false, false>(pl, st, a);
+}
+
+// Whether the split row solver's grid can be resident at once on the current device
+// (cooperative launch supported and enough workgroup slots); cached per device and size.
+bool split_fits(const void* kernel, size_t lds, int blocks) {
+  static std::mutex mu;
+  static const void* fns[64];
+  static int devs[64], nblk[64];
+  static size_t ldss[64];
+  static int n = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n; ++i)
+    if (fns[i] == kernel && devs[i] == dev && ldss[i] == lds) return nblk[i] >= blocks;
+  int coop = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess) coop = 0;
+  if (coop && hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, arbor::kBlock, lds) != hipSuccess)
+    per_cu = 0;
+  const int total = coop ? per_cu * device_cus() : 0;
+  if (n < 64) {
+    fns[n] = kernel;
+    devs[n] = dev;
+    ldss[n] = lds;
+    nblk[n] = total;
+    ++n;
+  }
+  return total >= blocks;
+}
+
+// The row solver: S workgroups per row when the plan splits rows and the grid can be
+// resident at once, else one workgroup per row.
+template <int DT>
+int launch_solver(const Plan& pl, hipStream_t st, arbor::Args a, char* ws) {
+  const size_t lds = arbor::solver_lds_bytes(pl.hash_bits);
+  const void* split = reinterpret_cast<const void*>(arbor::split_solver_kernel<DT>);
+  if (pl.S > 1) {
+    if (lds > 64 * 1024) {
+      const int r = allow_lds(split, lds);
+      if (r != ARBOR_OK) return r;
+    }
+    if (split_fits(split, lds, a.B * pl.S)) {
+      arbor::SplitChunk* chunks = reinterpret_cast<arbor::SplitChunk*>(ws + pl.off_split);
+      uint32_t* ctr = reinterpret_cast<uint32_t*>(ws + pl.off_ctr);
+      // the rows' barrier counters start at zero (a fill kernel: no memset node in a captured graph)
+      hipLaunchKernelGGL(arbor::zero_u32_kernel, dim3((unsigned)((a.B + 255) / 256)), dim3(256), 0, st, ctr, a.B);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return hip_fail(e, "kernel launch");
+      void* args[] = {&a, &chunks, &ctr};
+      e = hipLaunchCooperativeKernel(split, dim3((unsigned)(a.B * pl.S)), dim3(arbor::kBlock), args, (unsigned)lds, st);
+      if (e != hipSuccess) return hip_fail(e, "cooperative kernel launch");
+      return ARBOR_OK;
+    }
+  }
+  return launch(arbor::solver_kernel<DT>, dim3((unsigned)a.B), dim3(arbor::kBlock), lds, st, a);
 }
 
 }  // namespace
@@ -379,10 +452,8 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (pl.path == Path::Solver) {
-    const dim3 grid(p->batch), block(arbor::kBlock);
-    const size_t lds = arbor::solver_lds_bytes(pl.hash_bits);
-    if (p->dtype == ARBOR_DTYPE_BF16) return launch(arbor::solver_kernel<ARBOR_DTYPE_BF16>, grid, block, lds, s, a);
-    return launch(arbor::solver_kernel<ARBOR_DTYPE_F32>, grid, block, lds, s, a);
+    if (p->dtype == ARBOR_DTYPE_BF16) return launch_solver<ARBOR_DTYPE_BF16>(pl, s, a, ws);
+    return launch_solver<ARBOR_DTYPE_F32>(pl, s, a, ws);
   }
   const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
   if (p->dtype == ARBOR_DTYPE_BF16) return launch_topk<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a);

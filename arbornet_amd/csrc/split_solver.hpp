@@ -1,0 +1,454 @@
+// split_solver.hpp -- the exact general path (top-p without top-k, plain sampling, top-k
+// above the streaming limit) when the batch is smaller than the chip: S workgroups per
+// row, one chunk of ids each, launched cooperatively (so all of them are resident) and
+// meeting at per-row barriers between phases. Each phase reads only its own chunk of the
+// row (z is kept in the workspace) plus what the row's other chunks published.
+//
+//  1. Every workgroup builds the row's history table in LDS, writes its chunk of z
+//     (penalties applied to the chunk's history ids) and publishes the chunk's statistics.
+//  2. A cut (top-k by count, then top-p by mass; three barriers each): the chunks publish
+//     4096-bin histograms over d = zmax - z (the bins of mass_solver.hpp); every workgroup
+//     sums the row's S histograms and finds the bin holding the target, so all of them pick
+//     the same bin; the same within that bin; then the chunks publish the entries of the
+//     selected sub-bin and every workgroup ranks all of them and finds the same cut. More
+//     entries than kFsColl (heavy ties) send the row to the radix solver, which the row's
+//     first workgroup runs alone.
+//  3. The draw (one barrier): the chunks publish their kept fixed-point mass and last kept
+//     id; the workgroup whose chunk holds the crossing of floor(u * E) in id order scans it.
+// Masses are the fixed-point ones of mass_solver.hpp, so every sum is exact and the result
+// does not depend on the split.
+#pragma once
+
+#include "mass_solver.hpp"
+
+namespace arbor {
+
+// What one chunk of a row publishes (workspace, one record per workgroup).
+struct SplitChunk {
+  uint32_t kmax, kmin, nf, flags;  // order-key range of finite z, finite count, flags
+  unsigned long long kept_mass;     // fixed-point mass of the chunk's kept ids
+  int32_t kept_last;                // largest kept id of the chunk (-1: none)
+  int32_t ncoll;                    // entries of the selected sub-bin (may exceed kFsColl)
+  uint32_t cnt[kFsBins];
+  unsigned long long mass[kFsBins];
+  unsigned long long coll_key[kFsColl];
+  unsigned long long coll_m[kFsColl];
+};
+
+constexpr uint32_t kSplitSpinLimit = 1u << 26;  // seconds of waiting: a barrier that never fills is a bug
+
+// Barrier of the workgroups of one row. *ctr counts arrivals over the whole call (zeroed
+// before the launch); the n-th barrier of a row waits for n * S arrivals. Global writes
+// made before it are visible to the row's other workgroups after it (agent-scope release
+// before the arrival, acquire after the wait). A wait past the spin limit gives up and
+// sets *timed_out instead of hanging.
+__device__ __forceinline__ void row_barrier(uint32_t* ctr, uint32_t target, int* timed_out) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    atomicAdd(ctr, 1u);
+    uint32_t spins = 0u;
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins == kSplitSpinLimit) {
+        *timed_out = 1;
+        break;
+      }
+    }
+    __threadfence();
+  }
+  __syncthreads();
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk* chunks, uint32_t* ctr) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint32_t* htab = reinterpret_cast<uint32_t*>(smem);
+  FastShared& sh = *reinterpret_cast<FastShared*>(smem + ((sizeof(uint32_t) << a.hash_bits) + 15) / 16 * 16);
+  __shared__ int s_timeout;
+  constexpr int NW = kWaves;
+  const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
+  const int S = a.S, row = blockIdx.x / S, chunk = blockIdx.x % S;
+  const int V = a.V;
+  const int c0 = chunk * a.chunk_len, c1 = min(V, c0 + a.chunk_len), n = c1 - c0;
+  float* z = a.zbuf + (size_t)row * (size_t)a.ldz;  // the row's buffer; this workgroup owns [c0, c1)
+  const float* zc = z + c0;
+  SplitChunk* mine = chunks + blockIdx.x;
+  const SplitChunk* rowc = chunks + (size_t)row * (size_t)S;
+  const void* xrow = row_ptr<DT>(a, row);
+  const uint32_t* mrow = a.mask ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
+  const int P = 1 << a.hash_bits;
+  float* prow = a.write_probs ? a.out_probs + (size_t)row * (size_t)V : nullptr;
+  uint32_t passed = 0u;  // row barriers passed
+  if (t == 0) s_timeout = 0;
+  auto sync_row = [&]() { row_barrier(ctr + row, ++passed * (uint32_t)S, &s_timeout); };
+
+  // ---- 1. history table, the chunk's z, its statistics ----
+  uint32_t flags = 0u;
+  if (a.H > 0) {
+    for (int i = t; i < P; i += kBlock) htab[i] = kEmptySlot;
+    __syncthreads();
+    const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
+    for (int j = t; j < a.H; j += kBlock) {
+      const int32_t id = h[j];
+      if (id < 0) continue;
+      if (id >= V)
+        flags |= kFlagBadHistory;
+      else
+        hist_insert(htab, (uint32_t)a.hash_bits, (uint32_t)id);
+    }
+  }
+  fs_temper<kBlock, DT>(a, xrow, mrow, z, c0, c1);
+  __syncthreads();
+  if (a.H > 0) {
+    for (int sl = t; sl < P; sl += kBlock) {
+      const uint32_t e = htab[sl];
+      if (e == kEmptySlot) continue;
+      const int id = (int)(e >> 12);
+      if (id >= c0 && id < c1) z[id] = penalize(z[id], (e & 4095u) + 1u, a.pen);
+    }
+  }
+  __syncthreads();
+  {
+    uint32_t kmax = 0u, kmin = 0xFFFFFFFFu, nf = 0u;
+    fs_visit<kBlock>(zc, n, [&](int, float v) {
+      if (is_invalid(v)) flags |= kFlagInvalid;
+      if (v != -INFINITY && !is_invalid(v)) {
+        const uint32_t k = order_key(v);
+        kmax = k > kmax ? k : kmax;
+        kmin = k < kmin ? k : kmin;
+        ++nf;
+      }
+    });
+    flags = block_reduce_max<kBlock, uint32_t>(flags, sh.red32);
+    kmax = block_reduce_max<kBlock, uint32_t>(kmax, sh.red32);
+    kmin = block_reduce_min<kBlock, uint32_t>(kmin, sh.red32);
+    nf = block_reduce_sum<kBlock, uint32_t>(nf, sh.red32);
+    if (t == 0) {
+      mine->kmax = kmax;
+      mine->kmin = kmin;
+      mine->nf = nf;
+      mine->flags = flags;
+    }
+  }
+  sync_row();
+
+  // ---- row statistics (the same in every workgroup of the row) ----
+  uint32_t kmax = 0u, kmin = 0xFFFFFFFFu, nf = 0u, rflags = 0u;
+  for (int c = 0; c < S; ++c) {
+    kmax = max(kmax, rowc[c].kmax);
+    kmin = min(kmin, rowc[c].kmin);
+    nf += rowc[c].nf;
+    rflags |= rowc[c].flags;
+  }
+  bool skip = false;  // this workgroup has nothing more to compute (it still meets every barrier)
+  if (rflags != 0u || nf == 0u) {
+    if (chunk == 0 && t == 0)
+      a.out_ids[row] = (rflags & kFlagBadHistory) ? ARBOR_ID_BAD_HISTORY
+                                                   : ((rflags & kFlagInvalid) ? ARBOR_ID_INVALID : ARBOR_ID_EMPTY);
+    if (prow)
+      for (int i = c0 + t; i < c1; i += kBlock) prow[i] = 0.0f;
+    skip = true;
+  }
+  const float zmax = key_value(kmax);
+  const float span = fminf(zmax - key_value(kmin), kFsSpan);
+  const float scale = (float)kFsBins / fmaxf(span, 0x1p-20f);
+
+  // ---- 2. one cut over the split row (three barriers) ----
+  auto split_cut = [&](bool by_mass, uint64_t target, double frac) -> FsCut {
+    FsCut r{0ull, 0ull, 0ull, false};
+    uint64_t above_w = 0, above_c = 0, above_m = 0;
+    int b0 = 0, b1 = 0;
+    bool all = false;  // the whole row is below the target: keep everything
+    for (int level = 0; level < 2; ++level) {
+      if (!skip && !all) {
+        for (int i = t; i < kFsBins; i += kBlock) {
+          sh.cnt[i] = 0u;
+          sh.mass[i] = 0ull;
+        }
+        __syncthreads();
+        fs_visit<kBlock>(zc, n, [&](int, float v) {
+          if (v == -INFINITY) return;
+          const float x = fs_x(v, zmax, scale);
+          int d = fs_bin0(x);
+          if (level == 1) {
+            if (d != b0) return;
+            d = fs_bin1(x, b0);
+          }
+          atomicAdd(&sh.cnt[d], 1u);
+          atomicAdd(&sh.mass[d], (unsigned long long)mass_fixed(rel_exp(v, zmax)));
+        });
+        __syncthreads();
+        for (int i = t; i < kFsBins; i += kBlock) {
+          mine->cnt[i] = sh.cnt[i];
+          mine->mass[i] = sh.mass[i];
+        }
+      }
+      sync_row();
+      if (!skip && !all) {
+        // the row's histogram: the sum of its chunks'
+        for (int i = t; i < kFsBins; i += kBlock) {
+          uint32_t cn = 0u;
+          unsigned long long ms = 0ull;
+          for (int c = 0; c < S; ++c) {
+            cn += rowc[c].cnt[i];
+            ms += rowc[c].mass[i];
+          }
+          sh.cnt[i] = cn;
+          sh.mass[i] = ms;
+        }
+        __syncthreads();
+        if (level == 0 && frac > 0.0) {
+          uint64_t m = 0;
+          for (int b = t; b < kFsBins; b += kBlock) m += sh.mass[b];
+          m = fs_sum<kBlock>(m, sh.red64);
+          const double tg = ceil(frac * (double)m);
+          target = tg < 1.0 ? 1ull : (uint64_t)tg;
+          if (target > m) target = m;
+        }
+        uint64_t above;
+        const int b = fs_find_bin<kBlock>(sh, by_mass, target - above_w, &above);
+        if (b < 0) {
+          all = true;
+        } else {
+          uint64_t ac = 0, am = 0;
+          for (int j = t; j < kFsBins; j += kBlock)
+            if (j < b) {
+              ac += sh.cnt[j];
+              am += sh.mass[j];
+            }
+          ac = fs_sum<kBlock>(ac, sh.red64);
+          am = fs_sum<kBlock>(am, sh.red64);
+          above_w += above;
+          above_c += ac;
+          above_m += am;
+          if (level == 0)
+            b0 = b;
+          else
+            b1 = b;
+        }
+      }
+    }
+    // the chunk's entries of the selected sub-bin
+    if (!skip && !all) {
+      if (t == 0) sh.b32[1] = 0;
+      __syncthreads();
+      fs_visit<kBlock>(zc, n, [&](int i, float v) {
+        if (v == -INFINITY) return;
+        const float x = fs_x(v, zmax, scale);
+        if (fs_bin0(x) != b0 || fs_bin1(x, b0) != b1) return;
+        const int pos = atomicAdd(&sh.b32[1], 1);
+        if (pos < kFsColl) {
+          mine->coll_key[pos] = composite(v, c0 + i);
+          mine->coll_m[pos] = mass_fixed(rel_exp(v, zmax));
+        }
+      });
+      __syncthreads();
+      if (t == 0) mine->ncoll = sh.b32[1];
+    }
+    sync_row();
+    if (skip || all) return r;
+    // every chunk's entries, in chunk order, ranked by counting
+    int ntot = 0;
+    for (int c = 0; c < S; ++c) {
+      const int nc = rowc[c].ncoll;
+      if (nc > kFsColl || ntot + nc > kFsColl) {
+        r.tied = true;
+        return r;
+      }
+      for (int j = t; j < nc; j += kBlock) {
+        const unsigned long long m = rowc[c].coll_m[j];
+        sh.coll_key[ntot + j] = rowc[c].coll_key[j];
+        sh.coll_m[ntot + j] = m;
+        sh.coll_w[ntot + j] = by_mass ? m : 1ull;
+      }
+      ntot += nc;
+    }
+    __syncthreads();
+    if (t < ntot) {
+      const uint64_t c = sh.coll_key[t];
+      int rank = 0;
+      for (int j = 0; j < ntot; ++j) rank += sh.coll_key[j] > c ? 1 : 0;
+      sh.mass[2 * rank] = c;
+      sh.mass[2 * rank + 1] = (unsigned long long)t;
+    }
+    __syncthreads();
+    uint64_t w = 0, m = 0, c = 0;
+    if (t < ntot) {
+      const int idx = (int)sh.mass[2 * t + 1];
+      c = sh.mass[2 * t];
+      w = sh.coll_w[idx];
+      m = sh.coll_m[idx];
+    }
+    uint64_t totw, totm;
+    const uint64_t exw = fs_scan_excl<kBlock>(w, sh.red64, &totw);
+    const uint64_t exm = fs_scan_excl<kBlock>(m, sh.red64, &totm);
+    if (t == 0) sh.b32[2] = -1;
+    __syncthreads();
+    if (t < ntot && above_w + exw < target && above_w + exw + w >= target) {
+      sh.b32[2] = t;
+      sh.b64[1] = c;
+      sh.b64[2] = above_c + (uint64_t)t + 1;
+      sh.b64[3] = above_m + exm + m;
+    }
+    __syncthreads();
+    if (sh.b32[2] >= 0) {
+      r.cut = sh.b64[1];
+      r.count = sh.b64[2];
+      r.mass = sh.b64[3];
+    }
+    __syncthreads();
+    return r;
+  };
+
+  // cuts: top-k (count), then top-p (mass of the top-k survivors). Whether a cut runs is
+  // decided from the arguments and the row statistics, so every workgroup of the row
+  // meets the same barriers.
+  uint64_t cut = 0ull;
+  bool tied = false;
+  uint64_t kept_mass = 0ull;
+  if (a.top_k > 0 && (uint32_t)a.top_k < nf) {
+    const FsCut ck = split_cut(false, (uint64_t)a.top_k, 0.0);
+    tied = ck.tied;
+    cut = ck.cut;
+    kept_mass = ck.mass;
+  }
+  if (!tied && a.top_p < 1.0f) {
+    FsCut cp;
+    if (cut != 0ull) {
+      const double tg = ceil((double)a.top_p * (double)kept_mass);
+      uint64_t target = tg < 1.0 ? 1ull : (uint64_t)tg;
+      if (target > kept_mass) target = kept_mass;
+      cp = split_cut(true, target, 0.0);
+    } else {
+      cp = split_cut(true, 0ull, (double)a.top_p);
+    }
+    tied = cp.tied;
+    if (cp.cut > cut) cut = cp.cut;
+  }
+  if (tied && !skip) {  // more entries in the final sub-bin than are ranked directly
+    if (chunk == 0) solve_row<kBlock, DT>(a, row, htab, *reinterpret_cast<SolverShared*>(sh.cnt));
+    skip = true;
+  }
+  const bool use_min_p = a.min_p > 0.0f;
+
+  // ---- 3. draw: the chunk's kept mass, by waves over contiguous id ranges ----
+  const int seg = (((n + NW - 1) / NW) + 4 * kWave - 1) / (4 * kWave) * (4 * kWave);
+  const int r0 = min(n, wave * seg), r1 = min(n, r0 + seg);
+  auto kept = [&](int i, float v, uint64_t* w) -> bool {  // i relative to c0
+    *w = 0ull;
+    if (i >= r1 || v == -INFINITY || composite(v, c0 + i) < cut) return false;
+    const float e = rel_exp(v, zmax);
+    if (use_min_p && !(e >= a.min_p)) return false;
+    *w = mass_fixed(e);
+    return true;
+  };
+  const fs_f4* zq = reinterpret_cast<const fs_f4*>(zc);
+  uint64_t ws = 0;
+  if (!skip) {
+    int32_t wl = -1;
+    for (int i0 = r0 + 4 * lane; i0 < r1; i0 += 4 * kWave * kFsLoads) {
+      fs_f4 v[kFsLoads];
+#pragma unroll
+      for (int u = 0; u < kFsLoads; ++u) {
+        const int i = i0 + 4 * kWave * u;
+        v[u] = i < r1 ? zq[i >> 2] : fs_f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      }
+#pragma unroll
+      for (int u = 0; u < kFsLoads; ++u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int i = i0 + 4 * kWave * u + c;
+          uint64_t w;
+          if (kept(i, v[u][c], &w)) wl = c0 + i;
+          ws += w;
+        }
+    }
+    ws = wave_sum(ws);
+    wl = wave_max(wl);
+    if (lane == 0) {
+      sh.wsum[wave] = ws;
+      sh.wlast[wave] = wl;
+    }
+    __syncthreads();
+    const uint64_t wsl = lane < NW ? sh.wsum[lane] : 0ull;
+    const uint64_t ec = wave_sum(wsl);
+    const int32_t lc = wave_max(lane < NW ? sh.wlast[lane] : -1);
+    if (t == 0) {
+      mine->kept_mass = ec;
+      mine->kept_last = lc;
+    }
+  }
+  sync_row();
+  if (skip) return;
+  uint64_t E = 0, before = 0;
+  int32_t last = -1;
+  for (int c = 0; c < S; ++c) {
+    const uint64_t m = rowc[c].kept_mass;
+    E += m;
+    if (c < chunk) before += m;
+    last = max(last, (int32_t)rowc[c].kept_last);
+  }
+  const double uE = (double)a.uniforms[row] * (double)E;
+  uint64_t target;
+  if (uE >= 0.0)
+    target = uE >= 18446744073709549568.0 ? ~0ull : (uint64_t)uE;
+  else
+    target = uE < 0.0 ? 0ull : ~0ull;  // NaN: no crossing
+  const uint64_t ec = mine->kept_mass;
+  if (before <= target && before + ec > target) {
+    // this chunk holds the crossing: the wave whose range holds it scans its range
+    const uint64_t wsl = lane < NW ? sh.wsum[lane] : 0ull;
+    const uint64_t wbefore = before + wave_sum(lane < wave ? wsl : 0ull);
+    if (t == 0) sh.b32[3] = -1;
+    __syncthreads();
+    if (wbefore <= target && wbefore + ws > target) {
+      uint64_t run = wbefore;
+      for (int i0 = r0; i0 < r1; i0 += 4 * kWave) {
+        const int i = i0 + 4 * lane;
+        const fs_f4 v = i < r1 ? zq[i >> 2] : fs_f4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        uint64_t w[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kept(i + c, v[c], &w[c]);
+        const uint64_t lw = w[0] + w[1] + w[2] + w[3];
+        const uint64_t incl = run + wave_scan_incl(lw);
+        const uint64_t hit = __ballot(incl > target);
+        if (hit) {
+          if (lane == __ffsll((long long)hit) - 1) {
+            const uint64_t acc = incl - lw;
+            int pick = i + 3;
+#pragma unroll
+            for (int c = 3; c >= 0; --c)
+              if (acc + w[0] + (c > 0 ? w[1] : 0) + (c > 1 ? w[2] : 0) + (c > 2 ? w[3] : 0) > target) pick = i + c;
+            sh.b32[3] = c0 + pick;
+          }
+          break;
+        }
+        run = lane_get(incl, kWave - 1);
+      }
+    }
+    __syncthreads();
+    if (t == 0) a.out_ids[row] = sh.b32[3] >= 0 ? sh.b32[3] : last;
+  } else if (target >= E && last >= c0 && last < c1) {
+    if (t == 0) a.out_ids[row] = last;  // no crossing (u * E rounds to E or u is NaN): the last kept id
+  }
+  if (s_timeout && t == 0) a.out_ids[row] = ARBOR_ID_INVALID;  // a barrier gave up: never expected
+  if (prow) {
+    const double Ed = (double)E / (double)kMassScale;
+    fs_visit<kBlock>(zc, n, [&](int i, float v) {
+      float q = 0.0f;
+      if (v != -INFINITY && composite(v, c0 + i) >= cut) {
+        const float e = rel_exp(v, zmax);
+        if (!use_min_p || e >= a.min_p) q = (float)((double)e / Ed);
+      }
+      prow[c0 + i] = q;
+    });
+  }
+}
+
+__global__ void zero_u32_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+}  // namespace arbor

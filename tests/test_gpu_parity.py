@@ -135,15 +135,17 @@ def test_ties_lowest_id_wins(kw):
 
 @pytest.mark.parametrize("kw", [dict(top_p=0.5), dict(top_k=300), dict(top_k=3000, top_p=0.9)])
 @pytest.mark.parametrize("rounded", [False, True])
-def test_solver_many_ties(kw, rounded):
+@pytest.mark.parametrize("V", [5000, 40000])
+def test_solver_many_ties(kw, rounded, V):
     # More tied entries at the cut than the row solver ranks directly (1024): all-equal
-    # rows, and integer-valued logits (thousands of exact ties per value).
-    B, V = 4, 5000
+    # rows, and integer-valued logits (thousands of exact ties per value). V = 40000 puts
+    # each row on several workgroups (the split solver).
+    B = 4
     if rounded:
         inp = _random_inputs(B, V, seed=23, ties=True)
     else:
         inp = syn.Inputs(np.zeros((B, V), np.float32), None, None, np.array([0.0, 0.3, 0.7, 0.999], np.float32))
-    _announce(f"[solver ties] rounded={rounded} {kw}")
+    _announce(f"[solver ties] V={V} rounded={rounded} {kw}")
     ids, probs = run_gpu(_params(B, V, inp, **kw), inp, write_probs=True)
     compare(_params(B, V, inp, **kw), inp, ids, probs, label=f"solver-ties{kw}{rounded}")
 
