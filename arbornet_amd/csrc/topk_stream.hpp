@@ -446,8 +446,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       const float tn = fmaxf(ts, tc);
       if (tn > thr) set_thr(tn);
     };
-    set_thr(-FLT_MAX);
-    refresh();
+    set_thr(-FLT_MAX);  // the stream loop refreshes before its first batch
     // batches are interleaved over the streaming waves (wave w takes w, w + 15, ...)
     int nextb = wave + 3 * kTkStream;
     auto grab = [&]() -> int {
