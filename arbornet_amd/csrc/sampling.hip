@@ -110,6 +110,19 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
   }
 }
 
+// One generation step's history update: each row's sampled id (sentinels excluded) goes
+// to slot positions[b] mod H of the row's ring, and positions[b] advances. Penalties
+// count occurrences, so the ring's order does not matter.
+__global__ void append_kernel(int32_t* history, int H, int32_t* positions, const int32_t* ids, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int32_t id = ids[b];
+  if (id < 0) return;
+  const uint32_t pos = (uint32_t)positions[b];
+  history[(size_t)b * (size_t)H + pos % (uint32_t)H] = id;
+  positions[b] = (int32_t)(pos + 1u);
+}
+
 }  // namespace arbor
 
 // =======================================================================================
@@ -458,6 +471,23 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
   if (p->dtype == ARBOR_DTYPE_BF16) return launch_topk<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a);
   return launch_topk<ARBOR_DTYPE_F32>(pl, pen, mask, s, a);
+}
+
+int arbor_sample_append(const arbor_sampling_params* p, const void* logits, int32_t* history, int32_t* positions,
+                        const uint32_t* allow_mask, const float* uniforms, int32_t* out_ids, float* out_probs,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  int st = validate(p);
+  if (st != ARBOR_OK) return st;
+  if (p->hist_len <= 0 || !history || !positions)
+    return fail(ARBOR_ERR_HISTORY, "a history ring (hist_len > 0) and positions are required");
+  st = arbor_sample(p, logits, history, allow_mask, uniforms, out_ids, out_probs, workspace, workspace_bytes, stream);
+  if (st != ARBOR_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(arbor::append_kernel, dim3((unsigned)((p->batch + 255) / 256)), dim3(256), 0, s, history,
+                     (int)p->hist_len, positions, out_ids, (int)p->batch);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return ARBOR_OK;
 }
 
 int arbor_device_count(int* count) {

@@ -112,6 +112,8 @@ def library() -> ctypes.CDLL:
         P = ctypes.POINTER(SamplingParams)
         lib.arbor_sample.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.arbor_sample.restype = i32
+        lib.arbor_sample_append.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+        lib.arbor_sample_append.restype = i32
         lib.arbor_sample_workspace_bytes.argtypes = [P]
         lib.arbor_sample_workspace_bytes.restype = sz
         lib.arbor_sampling_params_init.argtypes = [P, ctypes.c_int32, ctypes.c_int32]
@@ -159,6 +161,14 @@ def sample_raw(params: SamplingParams, logits: int, history: Optional[int], mask
     """Call arbor_sample with raw device addresses; returns the status (does not raise)."""
     return int(library().arbor_sample(ctypes.byref(params), logits, history, mask, uniforms, out_ids,
                                       out_probs, workspace, workspace_bytes_, stream))
+
+
+def sample_append_raw(params: SamplingParams, logits: int, history: int, positions: int, mask: Optional[int],
+                      uniforms: int, out_ids: int, out_probs: Optional[int], workspace: int,
+                      workspace_bytes_: int, stream: Optional[int]) -> int:
+    """Call arbor_sample_append with raw device addresses; returns the status."""
+    return int(library().arbor_sample_append(ctypes.byref(params), logits, history, positions, mask, uniforms,
+                                             out_ids, out_probs, workspace, workspace_bytes_, stream))
 
 
 _workspaces: dict = {}
@@ -248,3 +258,63 @@ def params_for(workload, write_probs: bool = False) -> SamplingParams:
         frequency_penalty=workload.frequency_penalty, presence_penalty=workload.presence_penalty,
         top_k=workload.top_k, top_p=workload.top_p, min_p=workload.min_p, hist_len=workload.hist_len,
         mask_words=workload.mask_words, flags=ARBOR_FLAG_WRITE_PROBS if write_probs else 0)
+
+
+class GenerationState:
+    """Per-row token history of a generation loop, resident on the device: a ring of
+    ``hist_len`` ids per row (-1 = empty) and the number of ids appended to each row.
+    ``step`` samples from the last position of the model's logits and appends the sampled
+    ids (arbor_sample_append), so that the next step's penalties count them. There is no
+    counterpart in the reference: its models' Forward (ArborNet.Models/GPT.cs:96-111,
+    Llama3.cs:67-74) returns [batch, seq, vocab] logits that nothing consumes."""
+
+    def __init__(self, batch: int, hist_len: int, device, prompt=None):
+        import torch
+
+        if hist_len <= 0:
+            raise ValueError("hist_len must be positive")
+        self.batch, self.hist_len, self.device = batch, hist_len, torch.device(device)
+        self.history = torch.full((batch, hist_len), -1, dtype=torch.int32, device=self.device)
+        self.positions = torch.zeros(batch, dtype=torch.int32, device=self.device)
+        if prompt is not None:  # [batch, P] prompt ids: the last hist_len of them seed the ring
+            prompt = torch.as_tensor(prompt, dtype=torch.int32)
+            tail = prompt[:, -hist_len:]
+            self.history[:, : tail.shape[1]] = tail.to(self.device)
+            self.positions.fill_(tail.shape[1] % hist_len)
+
+    def step(self, logits, uniforms, *, temperature: float = 1.0, repetition_penalty: float = 1.0,
+             frequency_penalty: float = 0.0, presence_penalty: float = 0.0, top_k: int = 0,
+             top_p: float = 1.0, min_p: float = 0.0, allow_mask=None, vocab: Optional[int] = None,
+             out_ids=None):
+        """Sample one id per row from ``logits`` ([batch, seq, vocab]: the last position is
+        used; or [batch, ld]) and append it to the history. Returns int32 ids [batch]."""
+        import torch
+
+        if logits.dim() == 3:
+            logits = logits[:, -1, :]
+        if logits.dim() != 2 or logits.stride(1) != 1:
+            raise ValueError("logits must be [batch, seq, vocab] or [batch, ld] with contiguous rows")
+        if logits.shape[0] != self.batch or logits.device != self.device:
+            raise ValueError("logits do not match this state's batch and device")
+        V = int(vocab) if vocab is not None else logits.shape[1]
+        dtype = {torch.float32: ARBOR_DTYPE_F32, torch.bfloat16: ARBOR_DTYPE_BF16}.get(logits.dtype)
+        if dtype is None:
+            raise ArborSamplingError(-4, f"logits dtype {logits.dtype} is not float32 or bfloat16")
+        p = SamplingParams.make(self.batch, V, ld_logits=logits.stride(0), dtype=dtype, temperature=temperature,
+                                repetition_penalty=repetition_penalty, frequency_penalty=frequency_penalty,
+                                presence_penalty=presence_penalty, top_k=top_k, top_p=top_p, min_p=min_p,
+                                hist_len=self.hist_len)
+        mask_ptr = None
+        if allow_mask is not None:
+            allow_mask = allow_mask.to(device=self.device).contiguous()
+            p.mask_words = allow_mask.shape[1]
+            mask_ptr = allow_mask.data_ptr()
+        uniforms = uniforms.to(device=self.device, dtype=torch.float32).contiguous()
+        if out_ids is None:
+            out_ids = torch.empty(self.batch, dtype=torch.int32, device=self.device)
+        need = workspace_bytes(p) or 256
+        ws = _workspace(self.device, need)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        check(sample_append_raw(p, logits.data_ptr(), self.history.data_ptr(), self.positions.data_ptr(), mask_ptr,
+                                uniforms.data_ptr(), out_ids.data_ptr(), None, ws.data_ptr(), ws.numel(), stream))
+        return out_ids

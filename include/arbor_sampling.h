@@ -115,6 +115,26 @@ int arbor_sample(const arbor_sampling_params* params, const void* logits,
                  const float* uniforms, int32_t* out_ids, float* out_probs,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * One generation step: arbor_sample, then each row's sampled id is appended to the row's
+ * device history ring, so that the next step's penalties count it.
+ *   logits      the last position of the model's [batch, seq, vocab] output: pass a
+ *               pointer to position seq - 1 of row 0 and ld_logits = seq * vocab (or the
+ *               [batch, ld_logits] logits of a model that emits one position)
+ *   history     [batch, hist_len] int32 ring (device; -1 = empty slot); hist_len > 0
+ *   positions   [batch] int32 (device): ids appended to each row so far; the sampled id
+ *               goes to slot positions[b] mod hist_len and positions[b] advances. Rows
+ *               whose result is a sentinel (ARBOR_ID_*) append nothing.
+ *   the other arguments as for arbor_sample.
+ * No counterpart in the reference: its models return [batch, seq, vocab] logits
+ * (ArborNet.Models/GPT.cs:96-111, Llama3.cs:67-74) and nothing consumes them; this is the
+ * step a generation loop around those Forward calls would make.
+ */
+int arbor_sample_append(const arbor_sampling_params* params, const void* logits,
+                        int32_t* history, int32_t* positions, const uint32_t* allow_mask,
+                        const float* uniforms, int32_t* out_ids, float* out_probs,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* Bytes of workspace arbor_sample needs for these params (0 if params are invalid).
  * No reference counterpart: the reference's kernels need no scratch (CudaBackend.cs:43-46). */
 size_t arbor_sample_workspace_bytes(const arbor_sampling_params* params);

@@ -196,3 +196,18 @@ def test_params_for_matches_workload():
     p = S.params_for(w)
     assert (p.batch, p.vocab, p.top_k, p.hist_len) == (256, 128256, 50, 1024)
     assert np.float32(p.top_p) == np.float32(0.95)
+
+
+def test_sample_append_argument_checks():
+    # rejected before anything reaches the device
+    lib = S.library()
+    p = S.SamplingParams.make(4, 1000, hist_len=8)
+    need = S.workspace_bytes(p)
+    assert S.sample_append_raw(p, 16, None, 16, None, 16, 16, None, 16, need, None) == -10  # no ring
+    assert S.sample_append_raw(p, 16, 16, None, None, 16, 16, None, 16, need, None) == -10  # no positions
+    q = S.SamplingParams.make(4, 1000)  # hist_len 0: nothing to append to
+    assert S.sample_append_raw(q, 16, 16, 16, None, 16, 16, None, 16, S.workspace_bytes(q), None) == -10
+    r = S.SamplingParams.make(4, 1000, hist_len=8, top_p=2.0)
+    assert S.sample_append_raw(r, 16, 16, 16, None, 16, 16, None, 16, 1 << 30, None) == -8
+    assert lib.arbor_sample_append(None, 16, 16, 16, None, 16, 16, None, 16, 1 << 30, None) == -1
+    assert b"history" in lib.arbor_last_error() or lib.arbor_last_error()
