@@ -29,8 +29,11 @@ struct SplitChunk {
   unsigned long long kept_mass;     // fixed-point mass of the chunk's kept ids
   int32_t kept_last;                // largest kept id of the chunk (-1: none)
   int32_t ncoll;                    // entries of the selected sub-bin (may exceed kFsColl)
-  uint32_t cnt[kFsBins];
-  unsigned long long mass[kFsBins];
+  // one histogram per level: a workgroup writes its level-1 histogram while others of the
+  // row may still be reading its level-0 one (the next write to a level's histogram comes
+  // two barriers later, after every reader has passed the barrier between)
+  uint32_t cnt[2][kFsBins];
+  unsigned long long mass[2][kFsBins];
   unsigned long long coll_key[kFsColl];
   unsigned long long coll_m[kFsColl];
 };
@@ -180,8 +183,8 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
         });
         __syncthreads();
         for (int i = t; i < kFsBins; i += kBlock) {
-          mine->cnt[i] = sh.cnt[i];
-          mine->mass[i] = sh.mass[i];
+          mine->cnt[level][i] = sh.cnt[i];
+          mine->mass[level][i] = sh.mass[i];
         }
       }
       sync_row();
@@ -191,8 +194,8 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
           uint32_t cn = 0u;
           unsigned long long ms = 0ull;
           for (int c = 0; c < S; ++c) {
-            cn += rowc[c].cnt[i];
-            ms += rowc[c].mass[i];
+            cn += rowc[c].cnt[level][i];
+            ms += rowc[c].mass[level][i];
           }
           sh.cnt[i] = cn;
           sh.mass[i] = ms;

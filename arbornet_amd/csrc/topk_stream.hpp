@@ -8,17 +8,18 @@
 // so little of the row's fixed work is left after its last byte arrives.
 //
 //  Set-up: the row's history ids are loaded first, then the first batch of logits of every
-//     streaming wave; the LDS is cleared and one barrier passed. Once the first batch has
-//     been sampled the next two are requested, and the history ids fill an LDS bitmap of
-//     the chunk's history ids and an id -> count table.
-//  A. Threshold: every streaming wave adds the maxima of its lanes over its first batch
-//     to an LDS histogram of 12-bit order-key prefixes and takes the lower edge of
-//     the bin that holds the k-th largest value added so far: the k-th largest of any
-//     subset of the row bounds the row's k-th largest from below. History ids are not
-//     excluded from this sample (their penalty is not known there), so thresholds taken
-//     from it are checked at the end: if the k-th best candidate is at or above the
-//     highest of them that any wave used, it was a lower bound too and nothing in the top
-//     k was skipped; otherwise the row is solved exactly (row_solver.hpp).
+//     streaming wave; the LDS is cleared and one barrier passed. While the first batch is
+//     in flight the history ids fill an LDS bitmap of the chunk's history ids (and, for a
+//     frequency penalty, an id -> count table); the streaming waves wait until all of
+//     them are in. Once the first batch has been sampled the next two are requested.
+//  A. Threshold: every streaming wave adds, for each lane, the final z (penalised if it
+//     is a history id) of the lane's largest value in its first batch to an LDS histogram
+//     of 12-bit order-key prefixes, and takes the lower edge of the bin that holds the
+//     k-th largest value added so far: these are values of distinct ids, so the k-th
+//     largest of them bounds the row's k-th best from below. Thresholds taken from raw
+//     values elsewhere (masked batches that overflow the stage) are recorded and checked
+//     at the end: if the k-th best candidate is at or above the highest of them, nothing
+//     in the top k was skipped; otherwise the row is solved exactly (row_solver.hpp).
 //  B. Stream: raw logits are compared with the raw image of the threshold (x >= thr * T
 //     lowered by a margin is implied by z = x * (1/T) >= thr); the slots that pass are
 //     compacted into a per-wave LDS stage with ballots, then tempered, penalised if they
@@ -56,9 +57,6 @@ constexpr int kSampleBits = 12;             // threshold histogram: top 12 bits 
 constexpr int kSampleBins = 1 << kSampleBits;
 constexpr int kBufferWord3 = 0x00020000;    // buffer resource word 3 (gfx9 family: 32-bit data format)
 constexpr int kBufferNt = 2;                // buffer load cache policy: non-temporal
-// Queue entries whose history status is not known yet have bit 31 of the id word clear
-// (it is set for every id < 2^31); the finisher penalises them.
-constexpr uint64_t kRawMark = 1ull << 31;
 static_assert((kTkQueue & (kTkQueue - 1)) == 0, "the ring size is a power of two");
 
 // 16-byte loads per lane per batch (three batches per lane in flight or in hand)
@@ -325,20 +323,6 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         }
         s.queue[slot] = 0ull;
       }
-      if (PEN && __ballot(lane < m && (c & kRawMark) == 0ull)) {
-        // entries queued before every streaming wave's history ids were in the table
-        if (lane == 0)
-          while (__atomic_load_n(&s.hready, __ATOMIC_RELAXED) < kTkStream) __builtin_amdgcn_s_sleep(1);
-        wave_lds_sync();
-        if (lane < m && (c & kRawMark) == 0ull) {
-          c |= kRawMark;
-          const int id = composite_id(c);
-          const int off = id - c0;
-          if ((L.bitmap[off >> 5] >> (off & 31)) & 1u)
-            c = hist_inline ? composite(penalize(composite_z(c), count_of(id), a.pen), id) : 0ull;
-          if (c != 0ull) sample_add(s.chist, (uint32_t)(c >> 32));
-        }
-      }
       head += (uint32_t)m;
       wave_lds_sync();
       if (lane == 0) __atomic_store_n(&s.q_head, head, __ATOMIC_RELAXED);
@@ -393,17 +377,13 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     exact = (flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid));
     if (exact && lane == 0) s.verdict = 0;
   } else {
-    // ---- A. the wave's lane maxima over its first batch join the sample; then the next
-    // two batches are requested ----
-    {
-      float lm = -INFINITY;
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) lm = fmaxf(lm, zsample(ia, ba, q));
-      sample_add(s.hist, order_key(lm + 0.0f));
-      wave_lds_sync();
-    }
-    load(ib, bb);
-    load(ic, bc);
+    // ---- A. the history ids go into the bitmap (and the count table) while the first
+    // batch is in flight; once every streaming wave's are in, the final z of each lane's
+    // largest value in its first batch joins the sample. These are values of distinct ids,
+    // so the k-th largest of the sample bounds the row's k-th best from below even when
+    // the largest logits are history ids that a penalty lowers (as in a generation loop,
+    // whose history holds the tokens just sampled). Then the next two batches are
+    // requested ----
     if (PEN) {
       bool badh = false;
 #pragma unroll
@@ -418,12 +398,37 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       }
       if (__ballot(badh) && lane == 0) atomicOr(&s.flags, kFlagBadHistory);
       wave_lds_sync();
-      if (lane == 0) atomicAdd(&s.hready, 1);
+      if (lane == 0) {
+        atomicAdd(&s.hready, 1);
+        // every streaming wave inserts before it waits, and none queues anything before
+        while (__atomic_load_n(&s.hready, __ATOMIC_RELAXED) < kTkStream) __builtin_amdgcn_s_sleep(1);
+      }
+      wave_lds_sync();
     }
+    {
+      float lm = -INFINITY;
+      int lq = 0;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const float v = zsample(ia, ba, q);
+        if (v > lm) {
+          lm = v;
+          lq = q;
+        }
+      }
+      if (PEN && lm > -INFINITY) {
+        const int id = id_of(ia, lq), off = id - c0;
+        if ((L.bitmap[off >> 5] >> (off & 31)) & 1u) lm = penalize(lm, count_of(id), a.pen);
+      }
+      sample_add(s.hist, order_key(lm + 0.0f));
+      wave_lds_sync();
+    }
+    load(ib, bb);
+    load(ic, bc);
 
     // ---- B. stream ----
     uint64_t* stage = L.stage + wave * kTkStage;
-    bool bad = false, hwait = PEN;
+    bool bad = false;
     // z >= thr is accepted; x >= x_thr is implied by z = fl(x * (1/T)) >= thr
     float thr = 0.0f, x_thr = 0.0f;
     auto set_thr = [&](float tv) {
@@ -455,7 +460,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       return b;
     };
     // queue the lanes' candidates (final z) for the finisher
-    auto emit = [&](bool tk, float v, int id, bool raw = false) {
+    auto emit = [&](bool tk, float v, int id) {
       const uint64_t m = __ballot(tk);
       if (!m) return;
       uint32_t base = 0u;
@@ -464,31 +469,10 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       if (tk) {
         const uint32_t p = base + (uint32_t)lanes_below(m);
         // the ring slot is free once the finisher has taken the entry kTkQueue places back
-        uint64_t c = composite(v + 0.0f, id);
-        if (raw)
-          c &= ~kRawMark;  // the finisher penalises it and counts its final z
-        else
-          sample_add(s.chist, (uint32_t)(c >> 32));
+        const uint64_t c = composite(v + 0.0f, id);
+        sample_add(s.chist, (uint32_t)(c >> 32));
         while (p - __atomic_load_n(&s.q_head, __ATOMIC_RELAXED) >= (uint32_t)kTkQueue) __builtin_amdgcn_s_sleep(1);
         __atomic_store_n(&s.queue[p & (kTkQueue - 1)], c, __ATOMIC_RELAXED);
-      }
-    };
-    // every streaming wave's history ids are in the bitmap and the table (hwait: not seen
-    // yet). Candidates found before are queued raw for the finisher, so no streaming wave
-    // waits for the others' history ids.
-    auto history_ready = [&]() -> bool {
-      if (hwait && __atomic_load_n(&s.hready, __ATOMIC_RELAXED) >= kTkStream) {
-        wave_lds_sync();
-        hwait = false;
-      }
-      return !hwait;
-    };
-    auto wait_history = [&]() {
-      if (hwait) {
-        if (lane == 0)
-          while (__atomic_load_n(&s.hready, __ATOMIC_RELAXED) < kTkStream) __builtin_amdgcn_s_sleep(1);
-        wave_lds_sync();
-        hwait = false;
       }
     };
     // final z of a candidate whose raw logit passed (id inside the chunk, z not NaN / +inf):
@@ -513,22 +497,17 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     // bound of the row's k-th best and becomes the wave's threshold (this bounds what is
     // queued while the threshold is still far below the row's k-th best).
     auto consider = [&](bool tk, float x, int id) {
-      const bool known = history_ready();
       float v = -INFINITY;
       if (tk) {
         v = x * a.inv_t;
         if (is_invalid(v)) {
           bad = true;  // NaN, +inf, or overflow to +inf
           tk = false;
-        } else if (known) {
+        } else {
           v = final_z(v, id);
         }
       }
       tk = tk && v >= thr;
-      if (!known) {  // raw z (a penalty only lowers it here): the finisher settles it
-        emit(tk, v, id, true);
-        return;
-      }
       if constexpr (band) {
         const float vm = wave_max(tk ? v : -FLT_MAX);
         if (vm + ln_lo > thr) {
@@ -645,7 +624,6 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     }
 
     // history ids a penalty may raise: the row's first chunk scores all of them
-    wait_history();
     if (own_hist) {
       // streaming waves take interleaved 64-slot slices of the table (a power of two >= 64)
       for (int sb = wave; sb * kWave < (1 << a.hash_bits); sb += kTkStream) {
