@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--config", default="c3", help="c1..c5 (c3 is the headline)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline budget")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--step", action="store_true",
+                    help="time the generation step (arbor_sample_append: sample, then append the ids to the "
+                         "row's history ring) instead of arbor_sample; needs a workload with history")
     ap.add_argument("--sets", type=int, default=0, help="input sets rotated (0 = auto)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="bytes of the device-to-device copy that gives the practical ceiling and "
@@ -114,11 +117,21 @@ def main():
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
 
+    if args.step and w.hist_len <= 0:
+        print(f"--step needs a workload with history; {args.config} has none", file=sys.stderr)
+        sys.exit(2)
+    positions = [torch.zeros(w.batch, dtype=torch.int32, device=dev) for _ in range(nsets)]
+
     def step(i):
         x, h, m, u = sets[i % nsets]
-        st = S.sample_raw(p, x.data_ptr(), None if h is None else h.data_ptr(),
-                          None if m is None else m.data_ptr(), u.data_ptr(), ids[i % nsets].data_ptr(),
-                          None, ws.data_ptr(), need, sh)
+        if args.step:  # the history tensor is the ring the sampled ids are appended to
+            st = S.sample_append_raw(p, x.data_ptr(), h.data_ptr(), positions[i % nsets].data_ptr(),
+                                     None if m is None else m.data_ptr(), u.data_ptr(), ids[i % nsets].data_ptr(),
+                                     None, ws.data_ptr(), need, sh)
+        else:
+            st = S.sample_raw(p, x.data_ptr(), None if h is None else h.data_ptr(),
+                              None if m is None else m.data_ptr(), u.data_ptr(), ids[i % nsets].data_ptr(),
+                              None, ws.data_ptr(), need, sh)
         if st != 0:
             S.check(st)
 
@@ -183,7 +196,7 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-        "traffic": traffic_from_profiles(args.config),
+        "traffic": None if args.step else traffic_from_profiles(args.config),
         "algorithmic_bytes": set_bytes,
         "launch_ms_mean": round(ms_per_step, 5),
         "event_pair_ms_mean": round(kernel_ms, 5),
@@ -229,7 +242,8 @@ def main():
         "config": {
             "workload": f"{args.config}: B={w.batch} V={w.vocab} {w.dtype} T={w.temperature} top_k={w.top_k} "
                         f"top_p={w.top_p} min_p={w.min_p} rep={w.repetition_penalty} freq={w.frequency_penalty} "
-                        f"pres={w.presence_penalty} H={w.hist_len} mask={w.has_mask}",
+                        f"pres={w.presence_penalty} H={w.hist_len} mask={w.has_mask}"
+                        + (" (generation step: sample + history-ring append)" if args.step else ""),
             "batch": w.batch,
             "vocab": w.vocab,
             "input_sets_rotated": nsets,
