@@ -110,6 +110,11 @@ EDGE = [
     (8, 32000, None, "bf16", 512, 0.0, dict(top_p=0.95, min_p=0.1, temperature=1.3)),
     (9, 5000, None, "f32", 0, 0.0, dict(top_k=50, top_p=0.95)),  # batch not a multiple of 8
     (3, 100000, None, "f32", 4096, 0.0, dict(top_k=40, repetition_penalty=1.5, frequency_penalty=0.1)),
+    # split row solver: strided rows, odd vocabularies, unaligned bf16 rows, masks
+    (6, 24577, 24580, "f32", 64, 0.0, dict(top_p=0.85, repetition_penalty=1.2)),
+    (5, 30001, 30003, "bf16", 0, 0.0, dict(top_p=0.9, temperature=0.9)),
+    (7, 50000, None, "f32", 128, 0.1, dict(top_k=200, top_p=0.95, presence_penalty=0.5)),
+    (4, 65537, None, "f32", 0, 0.0, dict(top_p=0.5, min_p=0.01)),
 ]
 
 
