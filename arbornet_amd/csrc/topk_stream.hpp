@@ -162,10 +162,15 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   // occurrence counts matter only to a frequency penalty; without one, the bitmap says all
   const bool counts = a.pen.fp != 0.0f;
   const bool table = own_hist || (hist_inline && counts);
+  // scored inline, the table needs only the repeats: an id's first occurrence sets its
+  // bitmap bit, later ones go to the table (count = 1 + repeats)
+  const bool repeats_only = hist_inline && counts;
   TkLds L(smem, PEN ? a.bitmap_words : 0);
   // occurrences of a history id (one whose bitmap bit is set)
   auto count_of = [&](int id) -> uint32_t {
-    return counts ? hist_count(L.htab, (uint32_t)a.hash_bits, (uint32_t)id) : 1u;
+    if (!counts) return 1u;
+    const uint32_t n = hist_count(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
+    return repeats_only ? 1u + n : n;
   };
 
   const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
@@ -392,8 +397,15 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         if (id >= a.V) {
           badh = true;
         } else if (id >= 0) {
-          if (id >= c0 && id < c1) atomicOr(&L.bitmap[(id - c0) >> 5], 1u << ((id - c0) & 31));
-          if (table) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
+          const bool in_chunk = id >= c0 && id < c1;
+          const uint32_t bit = 1u << ((id - c0) & 31);
+          if (repeats_only) {
+            if (in_chunk && (atomicOr(&L.bitmap[(id - c0) >> 5], bit) & bit))
+              hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
+          } else {
+            if (in_chunk) atomicOr(&L.bitmap[(id - c0) >> 5], bit);
+            if (table) hist_insert(L.htab, (uint32_t)a.hash_bits, (uint32_t)id);
+          }
         }
       }
       if (__ballot(badh) && lane == 0) atomicOr(&s.flags, kFlagBadHistory);
