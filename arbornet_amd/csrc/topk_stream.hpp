@@ -11,8 +11,8 @@
 //     streaming wave; the LDS is cleared and one barrier passed. While the first batch is
 //     in flight the history ids fill an LDS bitmap of the chunk's history ids (and, for a
 //     frequency penalty, a table of the repeated ids and their counts); the streaming
-//     waves wait until all of
-//     them are in. Once the first batch has been sampled the next two are requested.
+//     waves wait until all of them are in. Once the first batch has been sampled the next
+//     two are requested.
 //  A. Threshold: every streaming wave adds, for each lane, the final z (penalised if it
 //     is a history id) of the lane's largest value in its first batch to an LDS histogram
 //     of 12-bit order-key prefixes, and takes the lower edge of the bin that holds the
