@@ -158,7 +158,7 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
   const float scale = (float)kFsBins / fmaxf(span, 0x1p-20f);
 
   // ---- 2. one cut over the split row (three barriers) ----
-  auto split_cut = [&](bool by_mass, uint64_t target, double frac) -> FsCut {
+  auto split_cut = [&](bool by_mass, bool need_mass, uint64_t target, double frac) -> FsCut {
     FsCut r{0ull, 0ull, 0ull, false};
     uint64_t above_w = 0, above_c = 0, above_m = 0;
     int b0 = 0, b1 = 0;
@@ -178,8 +178,9 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
             if (d != b0) return;
             d = fs_bin1(x, b0);
           }
-          atomicAdd(&sh.cnt[d], 1u);
-          atomicAdd(&sh.mass[d], (unsigned long long)mass_fixed(rel_exp(v, zmax)));
+          // a mass cut needs no counts; a count cut needs masses only for a top-p after it
+          if (!by_mass) atomicAdd(&sh.cnt[d], 1u);
+          if (need_mass) atomicAdd(&sh.mass[d], (unsigned long long)mass_fixed(rel_exp(v, zmax)));
         });
         __syncthreads();
         for (int i = t; i < kFsBins; i += kBlock) {
@@ -189,16 +190,35 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
       }
       sync_row();
       if (!skip && !all) {
-        // the row's histogram: the sum of its chunks'
-        for (int i = t; i < kFsBins; i += kBlock) {
-          uint32_t cn = 0u;
-          unsigned long long ms = 0ull;
-          for (int c = 0; c < S; ++c) {
-            cn += rowc[c].cnt[level][i];
-            ms += rowc[c].mass[level][i];
-          }
-          sh.cnt[i] = cn;
-          sh.mass[i] = ms;
+        // the row's histogram: the sum of its chunks' (every load of a thread in flight at
+        // once: four bins, four chunks at a time)
+        constexpr int PER = kFsBins / kBlock;
+        uint32_t cn[PER] = {};
+        unsigned long long ms[PER] = {};
+        for (int c0s = 0; c0s < S; c0s += 4) {
+          uint32_t cv[4][PER];
+          unsigned long long mv[4][PER];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < PER; ++q) {
+              const int c = c0s + j < S ? c0s + j : c0s;
+              cv[j][q] = rowc[c].cnt[level][t + q * kBlock];
+              mv[j][q] = rowc[c].mass[level][t + q * kBlock];
+            }
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (c0s + j < S)
+#pragma unroll
+              for (int q = 0; q < PER; ++q) {
+                cn[q] += cv[j][q];
+                ms[q] += mv[j][q];
+              }
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          sh.cnt[t + q * kBlock] = cn[q];
+          sh.mass[t + q * kBlock] = ms[q];
         }
         __syncthreads();
         if (level == 0 && frac > 0.0) {
@@ -311,7 +331,7 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
   bool tied = false;
   uint64_t kept_mass = 0ull;
   if (a.top_k > 0 && (uint32_t)a.top_k < nf) {
-    const FsCut ck = split_cut(false, (uint64_t)a.top_k, 0.0);
+    const FsCut ck = split_cut(false, a.top_p < 1.0f, (uint64_t)a.top_k, 0.0);
     tied = ck.tied;
     cut = ck.cut;
     kept_mass = ck.mass;
@@ -322,9 +342,9 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
       const double tg = ceil((double)a.top_p * (double)kept_mass);
       uint64_t target = tg < 1.0 ? 1ull : (uint64_t)tg;
       if (target > kept_mass) target = kept_mass;
-      cp = split_cut(true, target, 0.0);
+      cp = split_cut(true, true, target, 0.0);
     } else {
-      cp = split_cut(true, 0ull, (double)a.top_p);
+      cp = split_cut(true, true, 0ull, (double)a.top_p);
     }
     tied = cp.tied;
     if (cp.cut > cut) cut = cp.cut;
