@@ -212,7 +212,9 @@ __device__ __forceinline__ uint32_t hist_slot(uint32_t id, uint32_t bits) {
 __device__ __forceinline__ bool hist_insert(uint32_t* tab, uint32_t bits, uint32_t id) {
   const uint32_t mask = (1u << bits) - 1u;
   uint32_t s = hist_slot(id, bits);
-  for (;;) {
+  // at most one pass: the table has at least twice as many slots as ids, so a pass always
+  // finds the id or a free slot; the bound only makes every probe finite
+  for (uint32_t n = 0; n <= mask; ++n) {
     uint32_t cur = tab[s];
     if (cur == kEmptySlot) {
       const uint32_t prev = atomicCAS(&tab[s], kEmptySlot, id << 12);
@@ -225,18 +227,20 @@ __device__ __forceinline__ bool hist_insert(uint32_t* tab, uint32_t bits, uint32
     }
     s = (s + 1u) & mask;
   }
+  return false;
 }
 
 // Occurrence count of `id` (0 if absent).
 __device__ __forceinline__ uint32_t hist_count(const uint32_t* tab, uint32_t bits, uint32_t id) {
   const uint32_t mask = (1u << bits) - 1u;
   uint32_t s = hist_slot(id, bits);
-  for (;;) {
+  for (uint32_t n = 0; n <= mask; ++n) {  // at most one pass (see hist_insert)
     const uint32_t cur = tab[s];
     if (cur == kEmptySlot) return 0u;
     if ((cur >> 12) == id) return (cur & 4095u) + 1u;
     s = (s + 1u) & mask;
   }
+  return 0u;
 }
 
 struct Penalty {

@@ -430,8 +430,11 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         }
       }
       if (PEN && lm > -INFINITY) {
+        // as in the stream: a history id is penalised, or (when a penalty may raise it, and
+        // the row's first chunk scores every history id at the end) left out
         const int id = id_of(ia, lq), off = id - c0;
-        if ((L.bitmap[off >> 5] >> (off & 31)) & 1u) lm = penalize(lm, count_of(id), a.pen);
+        if ((L.bitmap[off >> 5] >> (off & 31)) & 1u)
+          lm = hist_inline ? penalize(lm, count_of(id), a.pen) : -INFINITY;
       }
       sample_add(s.hist, order_key(lm + 0.0f));
       wave_lds_sync();

@@ -238,3 +238,36 @@ def test_sample_op_on_torch_tensors():
     with pytest.raises(S.ArborSamplingError) as ei:
         S.Sampling.sample(x, torch.from_numpy(inp.uniforms), temperature=0.0)
     assert ei.value.status == -5
+
+
+def _random_case(i):
+    """A seeded random parameter set (sizes small enough for the oracle)."""
+    rng = np.random.default_rng(1000 + i)
+    B = int(rng.integers(1, 10))
+    V = int(rng.choice([257, 1000, 4099, 12000, 32000, 50001]))
+    ld = V + int(rng.choice([0, 0, 3, 16]))
+    dtype = "bf16" if rng.random() < 0.3 else "f32"
+    H = int(rng.choice([0, 0, 8, 64, 512]))
+    mf = float(rng.choice([0.0, 0.0, 0.05, 0.5]))
+    kw = dict(temperature=float(rng.choice([0.5, 0.8, 1.0, 1.7])))
+    r = rng.random()
+    if r < 0.45:
+        kw["top_k"] = int(rng.choice([1, 5, 40, 64, 100, 2000]))
+    if rng.random() < 0.5:
+        kw["top_p"] = float(rng.choice([0.3, 0.9, 0.99]))
+    if rng.random() < 0.35:
+        kw["min_p"] = float(rng.choice([0.01, 0.1, 0.5]))
+    if H:
+        kw["repetition_penalty"] = float(rng.choice([0.7, 1.0, 1.3]))
+        kw["frequency_penalty"] = float(rng.choice([0.0, 0.0, 0.4, -0.2]))
+        kw["presence_penalty"] = float(rng.choice([0.0, 0.3]))
+    return B, V, ld, dtype, H, mf, kw
+
+
+@pytest.mark.parametrize("i", range(40))
+def test_random_parameter_sets(i):
+    B, V, ld, dtype, H, mf, kw = _random_case(i)
+    _announce(f"[random {i}] B={B} V={V} ld={ld} {dtype} H={H} mask={mf} {kw}")
+    inp = _random_inputs(B, V, ld=ld, dtype=dtype, H=H, mask_frac=mf, seed=2000 + i)
+    ids, probs = run_gpu(_params(B, V, inp, **kw), inp, write_probs=True)
+    compare(_params(B, V, inp, **kw), inp, ids, probs, label=f"random{i}")
