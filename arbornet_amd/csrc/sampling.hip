@@ -231,7 +231,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
     pl.lds_stream = arbor::TkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0);
   } else if (B < cus) {
-    // row solver over S workgroups per row (cooperative launch), never below 8K ids per chunk
+    // row solver over S workgroups per row, never below 8K ids per chunk
     int S = cus / B;
     const int by_len = (V + 8191) / 8192;
     if (S > by_len) S = by_len;
@@ -254,7 +254,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   if (pl.path == Path::Solver && pl.S > 1) {
     off = align_up(off + sizeof(arbor::SplitChunk) * (size_t)B * (size_t)pl.S, 256);
     pl.off_ctr = off;
-    off = align_up(off + sizeof(uint32_t) * (size_t)B, 256);
+    off = align_up(off + sizeof(uint32_t) * ((size_t)B + 1), 256);  // row barriers + ticket
   }
   pl.total = off;
   return pl;
@@ -330,7 +330,8 @@ int launch_topk(const Plan& pl, bool pen, bool mask, hipStream_t st, const arbor
 }
 
 // Whether the split row solver's grid can be resident at once on the current device
-// (cooperative launch supported and enough workgroup slots); cached per device and size.
+// (enough workgroup slots, so that every row's workgroups run together on an idle device;
+// the kernel's ticket order keeps it correct with fewer); cached per device and size.
 bool split_fits(const void* kernel, size_t lds, int blocks) {
   static std::mutex mu;
   static const void* fns[64];
@@ -342,11 +343,9 @@ bool split_fits(const void* kernel, size_t lds, int blocks) {
   std::lock_guard<std::mutex> lock(mu);
   for (int i = 0; i < n; ++i)
     if (fns[i] == kernel && devs[i] == dev && ldss[i] == lds) return nblk[i] >= blocks;
-  int coop = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess) coop = 0;
-  if (coop && hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, arbor::kBlock, lds) != hipSuccess)
-    per_cu = 0;
-  const int total = coop ? per_cu * device_cus() : 0;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, arbor::kBlock, lds) != hipSuccess) per_cu = 0;
+  const int total = per_cu * device_cus();
   if (n < 64) {
     fns[n] = kernel;
     devs[n] = dev;
@@ -371,13 +370,16 @@ int launch_solver(const Plan& pl, hipStream_t st, arbor::Args a, char* ws) {
     if (split_fits(split, lds, a.B * pl.S)) {
       arbor::SplitChunk* chunks = reinterpret_cast<arbor::SplitChunk*>(ws + pl.off_split);
       uint32_t* ctr = reinterpret_cast<uint32_t*>(ws + pl.off_ctr);
-      // the rows' barrier counters start at zero (a fill kernel: no memset node in a captured graph)
-      hipLaunchKernelGGL(arbor::zero_u32_kernel, dim3((unsigned)((a.B + 255) / 256)), dim3(256), 0, st, ctr, a.B);
+      // the rows' barrier counters and the ticket counter start at zero (a fill kernel: no
+      // memset node in a captured graph)
+      hipLaunchKernelGGL(arbor::zero_u32_kernel, dim3((unsigned)((a.B + 1 + 255) / 256)), dim3(256), 0, st, ctr,
+                         a.B + 1);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return hip_fail(e, "kernel launch");
-      void* args[] = {&a, &chunks, &ctr};
-      e = hipLaunchCooperativeKernel(split, dim3((unsigned)(a.B * pl.S)), dim3(arbor::kBlock), args, (unsigned)lds, st);
-      if (e != hipSuccess) return hip_fail(e, "cooperative kernel launch");
+      hipLaunchKernelGGL(arbor::split_solver_kernel<DT>, dim3((unsigned)(a.B * pl.S)), dim3(arbor::kBlock), lds, st, a,
+                         chunks, ctr);
+      e = hipGetLastError();
+      if (e != hipSuccess) return hip_fail(e, "kernel launch");
       return ARBOR_OK;
     }
   }

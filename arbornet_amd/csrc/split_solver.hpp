@@ -1,8 +1,15 @@
 // split_solver.hpp -- the exact general path (top-p without top-k, plain sampling, top-k
 // above the streaming limit) when the batch is smaller than the chip: S workgroups per
-// row, one chunk of ids each, launched cooperatively (so all of them are resident) and
-// meeting at per-row barriers between phases. Each phase reads only its own chunk of the
-// row (z is kept in the workspace) plus what the row's other chunks published.
+// row, one chunk of ids each, meeting at per-row barriers between phases. Each phase reads
+// only its own chunk of the row (z is kept in the workspace) plus what the row's other
+// chunks published.
+//
+// An ordinary launch, without co-residency: each workgroup takes its (row, chunk) from a
+// ticket counter when it starts, so the tickets handed out are always a prefix in start
+// order. Every row but the one holding the next ticket then has all of its workgroups
+// running, and those wait only for each other; the one partial row waits for workgroups
+// that start as soon as other rows finish and free their slots. So every barrier fills
+// whatever share of the chip the grid gets (at least S workgroup slots).
 //
 //  1. Every workgroup builds the row's history table in LDS, writes its chunk of z
 //     (penalties applied to the chunk's history ids) and publishes the chunk's statistics.
@@ -41,7 +48,7 @@ struct SplitChunk {
 constexpr uint32_t kSplitSpinLimit = 1u << 26;  // seconds of waiting: a barrier that never fills is a bug
 
 // Barrier of the workgroups of one row. *ctr counts arrivals over the whole call (zeroed
-// before the launch); the n-th barrier of a row waits for n * S arrivals. Global writes
+// before the launch, like the ticket counter); the n-th barrier of a row waits for n * S arrivals. Global writes
 // made before it are visible to the row's other workgroups after it (agent-scope release
 // before the arrival, acquire after the wait). A wait past the spin limit gives up and
 // sets *timed_out instead of hanging.
@@ -69,14 +76,19 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
   uint32_t* htab = reinterpret_cast<uint32_t*>(smem);
   FastShared& sh = *reinterpret_cast<FastShared*>(smem + ((sizeof(uint32_t) << a.hash_bits) + 15) / 16 * 16);
   __shared__ int s_timeout;
+  __shared__ uint32_t s_ticket;
   constexpr int NW = kWaves;
   const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
-  const int S = a.S, row = blockIdx.x / S, chunk = blockIdx.x % S;
+  // (row, chunk) in start order: ctr[B] is the ticket counter, ctr[0..B) the row barriers
+  if (t == 0) s_ticket = atomicAdd(ctr + a.B, 1u);
+  __syncthreads();
+  const int ticket = (int)s_ticket;
+  const int S = a.S, row = ticket / S, chunk = ticket % S;
   const int V = a.V;
   const int c0 = chunk * a.chunk_len, c1 = min(V, c0 + a.chunk_len), n = c1 - c0;
   float* z = a.zbuf + (size_t)row * (size_t)a.ldz;  // the row's buffer; this workgroup owns [c0, c1)
   const float* zc = z + c0;
-  SplitChunk* mine = chunks + blockIdx.x;
+  SplitChunk* mine = chunks + ticket;
   const SplitChunk* rowc = chunks + (size_t)row * (size_t)S;
   const void* xrow = row_ptr<DT>(a, row);
   const uint32_t* mrow = a.mask ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;

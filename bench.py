@@ -14,7 +14,9 @@ roofline    algorithmic bytes per call / average launch duration over the timed 
             with an event pair around every launch is reported beside it (those events add
             a gap per launch); copy_gbs = read+write rate of a device copy of one input set
 cpu_baseline  the C oracle (a scalar restatement of the step) on this host, 1 thread,
-            on a bounded sample of rows of the same workload
+            on a bounded sample of rows of the same workload; `parallel` beside it is the
+            same code with rows spread over the host's threads (the CPU share the box
+            grants: OMP_NUM_THREADS, else every core)
 """
 from __future__ import annotations
 
@@ -208,15 +210,19 @@ def main():
     if not args.no_cpu_baseline:
         from oracle import oracle
 
-        # bounded sample: whole batches of the same workload, single thread, ~cpu-seconds
-        rows = 0
-        t0 = time.perf_counter()
-        while True:
-            oracle.sample(p, inp.logits, inp.history, inp.mask, inp.uniforms, threads=1)
-            rows += w.batch
-            if time.perf_counter() - t0 >= args.cpu_seconds:
-                break
-        el = time.perf_counter() - t0
+        def timed(threads: int, seconds: float):
+            # bounded sample: whole batches of the same workload until `seconds` have passed
+            n = 0
+            t0 = time.perf_counter()
+            while True:
+                oracle.sample(p, inp.logits, inp.history, inp.mask, inp.uniforms, threads=threads)
+                n += w.batch
+                if time.perf_counter() - t0 >= seconds:
+                    return n, time.perf_counter() - t0
+
+        rows, el = timed(1, args.cpu_seconds)
+        nthr = max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or 10**6))
+        prows, pel = timed(nthr, max(1.0, args.cpu_seconds / 4))
         cpu = {
             "value": round(rows / el, 1),
             "unit": "rows/s",
@@ -224,6 +230,11 @@ def main():
             "kind": "port",
             "sample": f"{rows} rows ({rows // w.batch} full {args.config} batches) in {el:.1f} s, "
                       f"1 thread of {os.cpu_count()} ({cpu_model()}), inputs in host memory",
+            "parallel": {
+                "value": round(prows / pel, 1),
+                "threads": nthr,
+                "sample": f"{prows} rows in {pel:.1f} s, rows split over {nthr} threads",
+            },
         }
 
     out = {
