@@ -5,10 +5,11 @@
 // later pass reads it back from the caches. A cut (top-k by count, top-p by probability
 // mass) is found with two levels of 4096-bin histograms over the distance below the row
 // maximum, d = zmax - z: level 0 splits [0, span) into 4096 bins (span = min(zmax - zmin,
-// 32); beyond 32 every fixed-point mass is zero), level 1 splits the bin that holds the
-// target into 4096 more. Both bin functions are monotone in z (float rounding is
-// monotone), so bins are contiguous ranges of the rank order; the entries of the final
-// sub-bin are collected and ranked by their 64-bit rank key. Masses are fixed point
+// 32); beyond 32 every fixed-point mass is zero), and when the bin that holds the target
+// has more than kFsColl entries, level 1 splits it into 4096 more. Both bin functions are
+// monotone in z (float rounding is monotone), so bins are contiguous ranges of the rank
+// order; the entries of the final bin or sub-bin are collected and ranked by their 64-bit
+// rank key. Masses are fixed point
 // (exp(z - zmax) in units of 2^-40, summed in uint64), so every sum is exact and the cut
 // and the draw are the same as those of the radix solver (row_solver.hpp), which remains
 // the fallback for rows with more than kFsColl entries in one sub-bin (ties).
@@ -197,7 +198,8 @@ __device__ FsCut fs_cut(const float* z, int V, float zmax, float scale, bool by_
   const int t = threadIdx.x;
   FsCut r{0ull, 0ull, 0ull, false};
   uint64_t above_w = 0, above_c = 0, above_m = 0;
-  int b0 = 0, b1 = 0;  // selected bins
+  int b0 = 0, b1 = 0;    // selected bins
+  bool direct = false;  // the level-0 bin is collected whole (no level 1)
   for (int level = 0; level < 2; ++level) {
     for (int i = t; i < kFsBins; i += BLOCK) {
       sh.cnt[i] = 0u;
@@ -239,18 +241,26 @@ __device__ FsCut fs_cut(const float* z, int V, float zmax, float scale, bool by_
     above_w += above;
     above_c += ac;
     above_m += am;
-    if (level == 0)
+    if (level == 0) {
       b0 = b;
-    else
+      // a bin small enough to collect whole needs no level 1
+      const bool small = sh.cnt[b0] <= (uint32_t)kFsColl;
+      __syncthreads();  // every thread has read the count before level 1 clears the bins
+      if (small) {
+        direct = true;
+        break;
+      }
+    } else {
       b1 = b;
+    }
   }
-  // entries of the selected sub-bin: collect, rank by counting, run the target down
+  // entries of the selected bin or sub-bin: collect, rank by counting, run the target down
   if (t == 0) sh.b32[1] = 0;
   __syncthreads();
   fs_visit<BLOCK>(z, V, [&](int i, float v) {
     if (v == -INFINITY) return;
     const float x = fs_x(v, zmax, scale);
-    if (fs_bin0(x) != b0 || fs_bin1(x, b0) != b1) return;
+    if (fs_bin0(x) != b0 || (!direct && fs_bin1(x, b0) != b1)) return;
     const int pos = atomicAdd(&sh.b32[1], 1);
     if (pos < kFsColl) {
       const uint64_t m = mass_fixed(rel_exp(v, zmax));

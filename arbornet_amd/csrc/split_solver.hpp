@@ -13,11 +13,12 @@
 //
 //  1. Every workgroup builds the row's history table in LDS, writes its chunk of z
 //     (penalties applied to the chunk's history ids) and publishes the chunk's statistics.
-//  2. A cut (top-k by count, then top-p by mass; three barriers each): the chunks publish
-//     4096-bin histograms over d = zmax - z (the bins of mass_solver.hpp); every workgroup
-//     sums the row's S histograms and finds the bin holding the target, so all of them pick
-//     the same bin; the same within that bin; then the chunks publish the entries of the
-//     selected sub-bin and every workgroup ranks all of them and finds the same cut. More
+//  2. A cut (top-k by count, then top-p by mass; two or three barriers each): the chunks
+//     publish 4096-bin histograms over d = zmax - z (the bins of mass_solver.hpp); every
+//     workgroup sums the row's S histograms and finds the bin holding the target, so all of
+//     them pick the same bin; when that bin holds more than kFsColl entries, the same again
+//     within it; then the chunks publish the entries of the selected bin or sub-bin and
+//     every workgroup ranks all of them and finds the same cut. More
 //     entries than kFsColl (heavy ties) send the row to the radix solver, which the row's
 //     first workgroup runs alone.
 //  3. The draw (one barrier): the chunks publish their kept fixed-point mass and last kept
@@ -169,12 +170,13 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
   const float span = fminf(zmax - key_value(kmin), kFsSpan);
   const float scale = (float)kFsBins / fmaxf(span, 0x1p-20f);
 
-  // ---- 2. one cut over the split row (three barriers) ----
+  // ---- 2. one cut over the split row (two barriers, three when the level-0 bin is large) ----
   auto split_cut = [&](bool by_mass, bool need_mass, uint64_t target, double frac) -> FsCut {
     FsCut r{0ull, 0ull, 0ull, false};
     uint64_t above_w = 0, above_c = 0, above_m = 0;
     int b0 = 0, b1 = 0;
-    bool all = false;  // the whole row is below the target: keep everything
+    bool all = false;     // the whole row is below the target: keep everything
+    bool direct = false;  // the level-0 bin is collected whole (no level 1)
     for (int level = 0; level < 2; ++level) {
       if (!skip && !all) {
         for (int i = t; i < kFsBins; i += kBlock) {
@@ -190,8 +192,9 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
             if (d != b0) return;
             d = fs_bin1(x, b0);
           }
-          // a mass cut needs no counts; a count cut needs masses only for a top-p after it
-          if (!by_mass) atomicAdd(&sh.cnt[d], 1u);
+          // a mass cut needs counts only at level 0 (to size the selected bin); a count cut
+          // needs masses only for a top-p after it
+          if (!by_mass || level == 0) atomicAdd(&sh.cnt[d], 1u);
           if (need_mass) atomicAdd(&sh.mass[d], (unsigned long long)mass_fixed(rel_exp(v, zmax)));
         });
         __syncthreads();
@@ -263,6 +266,16 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
             b1 = b;
         }
       }
+      // a level-0 bin small enough to collect whole needs no level 1: every workgroup of the
+      // row summed the same counts, so all of them leave here or none
+      if (level == 0 && !skip && !all) {
+        const bool small = sh.cnt[b0] <= (uint32_t)kFsColl;
+        __syncthreads();  // every thread has read the count before level 1 clears the bins
+        if (small) {
+          direct = true;
+          break;
+        }
+      }
     }
     // the chunk's entries of the selected sub-bin
     if (!skip && !all) {
@@ -271,7 +284,7 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
       fs_visit<kBlock>(zc, n, [&](int i, float v) {
         if (v == -INFINITY) return;
         const float x = fs_x(v, zmax, scale);
-        if (fs_bin0(x) != b0 || fs_bin1(x, b0) != b1) return;
+        if (fs_bin0(x) != b0 || (!direct && fs_bin1(x, b0) != b1)) return;
         const int pos = atomicAdd(&sh.b32[1], 1);
         if (pos < kFsColl) {
           mine->coll_key[pos] = composite(v, c0 + i);

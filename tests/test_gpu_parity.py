@@ -155,6 +155,23 @@ def test_solver_many_ties(kw, rounded, V):
     compare(_params(B, V, inp, **kw), inp, ids, probs, label=f"solver-ties{kw}{rounded}")
 
 
+@pytest.mark.parametrize("kw", [dict(top_p=0.5), dict(top_k=3000), dict(top_k=3000, top_p=0.7)])
+@pytest.mark.parametrize("V", [5000, 40000])
+def test_solver_dense_bin(kw, V):
+    # One level-0 bin (a 4096th of the z span) holds nearly the whole row: distinct values
+    # spread over [0, 1e-3) and one outlier at -30, so the cut lies inside a bin with more
+    # entries than are collected directly and is found by the level-1 histogram.
+    # V = 40000 puts each row on several workgroups (the split solver).
+    B = 4
+    rng = np.random.default_rng(31)
+    x = (rng.random((B, V)) * 1e-3).astype(np.float32)
+    x[:, 7] = -30.0
+    inp = syn.Inputs(x, None, None, np.array([0.05, 0.3, 0.7, 0.95], np.float32))
+    _announce(f"[solver dense bin] V={V} {kw}")
+    ids, probs = run_gpu(_params(B, V, inp, **kw), inp, write_probs=True)
+    compare(_params(B, V, inp, **kw), inp, ids, probs, label=f"solver-dense{kw}")
+
+
 def test_sentinels():
     B, V = 6, 3000
     inp = _random_inputs(B, V, H=8, mask_frac=0.5, seed=7)
