@@ -141,6 +141,59 @@ __device__ __forceinline__ void fs_temper(const Args& a, const void* xrow, const
   }
 }
 
+// fs_temper with the penalties and the statistics in the same pass: ids whose bit
+// (i - c0) is set in hbits are history ids (counts from the row's history table) and are
+// penalised as they are written, with the same operations in the same order as a
+// separate penalty pass over z. Returns, over the written z: the order-key range and the
+// number of finite entries, and whether any entry is invalid (NaN or +inf).
+template <int BLOCK, int DT>
+__device__ __forceinline__ void fs_temper_stats(const Args& a, const void* xrow, const uint32_t* mrow,
+                                                const uint32_t* hbits, const uint32_t* htab, float* z, int c0,
+                                                int c1, uint32_t& kmax, uint32_t& kmin, uint32_t& nf, bool& invalid) {
+  constexpr int VEC = Elem<DT>::kVec;
+  static_assert(32 % VEC == 0, "a unit's history bits lie in one bitmap word");
+  const bool aligned = a.aligned != 0;
+  const int nu = (c1 - c0 + VEC - 1) / VEC;
+  for (int base = threadIdx.x; base < nu; base += BLOCK * kFsLoads) {
+    float x[kFsLoads][VEC];
+#pragma unroll
+    for (int u = 0; u < kFsLoads; ++u) {
+      const int q = base + u * BLOCK;
+      if (q < nu) load_unit<DT>(xrow, c0 + q * VEC, c1, aligned, x[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kFsLoads; ++u) {
+      const int q = base + u * BLOCK;
+      if (q >= nu) continue;
+      const int e0 = c0 + q * VEC;
+      const uint32_t bits = mrow ? mrow[e0 >> 5] >> (e0 & 31) : 0xFFFFFFFFu;
+      const uint32_t hb = hbits ? hbits[(e0 - c0) >> 5] >> ((e0 - c0) & 31) : 0u;
+#pragma unroll
+      for (int c = 0; c < VEC; c += 4) {
+        fs_f4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float v = x[u][c + j] * a.inv_t + 0.0f;
+          v = ((bits >> (c + j)) & 1u) ? v : -INFINITY;
+          if ((hb >> (c + j)) & 1u) v = penalize(v, hist_count(htab, (uint32_t)a.hash_bits, (uint32_t)(e0 + c + j)), a.pen);
+          o[j] = v;
+          if (e0 + c + j < c1) {
+            const bool bad = is_invalid(v);
+            invalid |= bad;
+            if (v != -INFINITY && !bad) {
+              const uint32_t k = order_key(v);
+              kmax = k > kmax ? k : kmax;
+              kmin = k < kmin ? k : kmin;
+              ++nf;
+            }
+          }
+        }
+        if (e0 + c < c1) *reinterpret_cast<fs_f4*>(z + e0 + c) = o;
+      }
+    }
+  }
+}
+
 // Level-0 bin of d = zmax - v (scale = kFsBins / span), and the level-1 sub-bin of an
 // entry of level-0 bin b0. Non-decreasing in d, i.e. bins ascend as the rank descends.
 __device__ __forceinline__ float fs_x(float v, float zmax, float scale) { return (zmax - v) * scale; }
@@ -325,45 +378,61 @@ __device__ void solve_row_fast(const Args& a, int row, uint32_t* htab, FastShare
   const uint32_t* mrow = a.mask ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
   const int P = 1 << a.hash_bits;
 
-  // 1. history table of the whole row
+  // 1. history table of the whole row, and its ids as a bitmap (in the histograms' mass
+  // array, unused until the first cut) when the row fits in it. fp32 rows only: with bf16
+  // units (8 entries) the fused pass spills in this kernel.
   uint32_t flags = 0;
+  const bool fused = DT == ARBOR_DTYPE_F32 && V <= 64 * kFsBins;
+  uint32_t* hbits = fused && a.H > 0 ? reinterpret_cast<uint32_t*>(sh.mass) : nullptr;
   if (a.H > 0) {
     for (int i = t; i < P; i += BLOCK) htab[i] = kEmptySlot;
+    if (hbits)
+      for (int i = t; i < (V + 31) / 32; i += BLOCK) hbits[i] = 0u;
     __syncthreads();
     const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
     for (int j = t; j < a.H; j += BLOCK) {
       const int32_t id = h[j];
       if (id < 0) continue;
-      if (id >= V)
+      if (id >= V) {
         flags |= kFlagBadHistory;
-      else
+      } else {
         hist_insert(htab, (uint32_t)a.hash_bits, (uint32_t)id);
+        if (hbits) atomicOr(&hbits[id >> 5], 1u << (id & 31));
+      }
     }
   }
-  // 2. tempered, masked logits
-  fs_temper<BLOCK, DT>(a, xrow, mrow, z, 0, V);
-  __syncthreads();
-  // 3. penalties, one writer per distinct history id
-  if (a.H > 0) {
-    for (int s = t; s < P; s += BLOCK) {
-      const uint32_t e = htab[s];
-      if (e == kEmptySlot) continue;
-      const uint32_t id = e >> 12;
-      z[id] = penalize(z[id], (e & 4095u) + 1u, a.pen);
-    }
-  }
-  __syncthreads();
-  // 4. row statistics
   uint32_t kmax = 0, kmin = 0xFFFFFFFFu, nf = 0;
-  fs_visit<BLOCK>(z, V, [&](int, float v) {
-    if (is_invalid(v)) flags |= kFlagInvalid;
-    if (v != -INFINITY && !is_invalid(v)) {
-      const uint32_t k = order_key(v);
-      kmax = k > kmax ? k : kmax;
-      kmin = k < kmin ? k : kmin;
-      ++nf;
+  if (fused) {
+    // 2-4. tempered, masked, penalised logits and the row statistics in one pass
+    __syncthreads();  // history table and bitmap complete
+    bool invalid = false;
+    fs_temper_stats<BLOCK, DT>(a, xrow, mrow, hbits, htab, z, 0, V, kmax, kmin, nf, invalid);
+    if (invalid) flags |= kFlagInvalid;
+  } else {
+    // 2. tempered, masked logits
+    fs_temper<BLOCK, DT>(a, xrow, mrow, z, 0, V);
+    __syncthreads();
+    // 3. penalties, one writer per distinct history id
+    if (a.H > 0) {
+      for (int s = t; s < P; s += BLOCK) {
+        const uint32_t e = htab[s];
+        if (e == kEmptySlot) continue;
+        const uint32_t id = e >> 12;
+        z[id] = penalize(z[id], (e & 4095u) + 1u, a.pen);
+      }
     }
-  });
+    __syncthreads();
+    // 4. row statistics
+    fs_visit<BLOCK>(z, V, [&](int, float v) {
+      if (is_invalid(v)) flags |= kFlagInvalid;
+      if (v != -INFINITY && !is_invalid(v)) {
+        const uint32_t k = order_key(v);
+        kmax = k > kmax ? k : kmax;
+        kmin = k < kmin ? k : kmin;
+        ++nf;
+      }
+    });
+  }
   flags = block_reduce_max<BLOCK, uint32_t>(flags & kFlagBadHistory ? 2u : (flags & kFlagInvalid ? 1u : 0u),
                                             sh.red32);
   kmax = block_reduce_max<BLOCK, uint32_t>(kmax, sh.red32);

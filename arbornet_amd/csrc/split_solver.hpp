@@ -101,41 +101,57 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
 
   // ---- 1. history table, the chunk's z, its statistics ----
   uint32_t flags = 0u;
+  // The chunk's history ids as a bitmap (in the histograms' mass array, unused until the
+  // first cut) when it fits, so that penalties and statistics come with the one pass over
+  // the logits; longer chunks penalise z in place and read it back for the statistics.
+  const bool fused = n <= 64 * kFsBins;
+  uint32_t* hbits = fused && a.H > 0 ? reinterpret_cast<uint32_t*>(sh.mass) : nullptr;
   if (a.H > 0) {
     for (int i = t; i < P; i += kBlock) htab[i] = kEmptySlot;
+    if (hbits)
+      for (int i = t; i < (n + 31) / 32; i += kBlock) hbits[i] = 0u;
     __syncthreads();
     const int32_t* h = a.hist + (size_t)row * (size_t)a.H;
     for (int j = t; j < a.H; j += kBlock) {
       const int32_t id = h[j];
       if (id < 0) continue;
-      if (id >= V)
+      if (id >= V) {
         flags |= kFlagBadHistory;
-      else
+      } else {
         hist_insert(htab, (uint32_t)a.hash_bits, (uint32_t)id);
+        if (hbits && id >= c0 && id < c1) atomicOr(&hbits[(id - c0) >> 5], 1u << ((id - c0) & 31));
+      }
     }
   }
-  fs_temper<kBlock, DT>(a, xrow, mrow, z, c0, c1);
-  __syncthreads();
-  if (a.H > 0) {
-    for (int sl = t; sl < P; sl += kBlock) {
-      const uint32_t e = htab[sl];
-      if (e == kEmptySlot) continue;
-      const int id = (int)(e >> 12);
-      if (id >= c0 && id < c1) z[id] = penalize(z[id], (e & 4095u) + 1u, a.pen);
-    }
-  }
-  __syncthreads();
   {
     uint32_t kmax = 0u, kmin = 0xFFFFFFFFu, nf = 0u;
-    fs_visit<kBlock>(zc, n, [&](int, float v) {
-      if (is_invalid(v)) flags |= kFlagInvalid;
-      if (v != -INFINITY && !is_invalid(v)) {
-        const uint32_t k = order_key(v);
-        kmax = k > kmax ? k : kmax;
-        kmin = k < kmin ? k : kmin;
-        ++nf;
+    if (fused) {
+      __syncthreads();  // history table and bitmap complete
+      bool invalid = false;
+      fs_temper_stats<kBlock, DT>(a, xrow, mrow, hbits, htab, z, c0, c1, kmax, kmin, nf, invalid);
+      if (invalid) flags |= kFlagInvalid;
+    } else {
+      fs_temper<kBlock, DT>(a, xrow, mrow, z, c0, c1);
+      __syncthreads();
+      if (a.H > 0) {
+        for (int sl = t; sl < P; sl += kBlock) {
+          const uint32_t e = htab[sl];
+          if (e == kEmptySlot) continue;
+          const int id = (int)(e >> 12);
+          if (id >= c0 && id < c1) z[id] = penalize(z[id], (e & 4095u) + 1u, a.pen);
+        }
       }
-    });
+      __syncthreads();
+      fs_visit<kBlock>(zc, n, [&](int, float v) {
+        if (is_invalid(v)) flags |= kFlagInvalid;
+        if (v != -INFINITY && !is_invalid(v)) {
+          const uint32_t k = order_key(v);
+          kmax = k > kmax ? k : kmax;
+          kmin = k < kmin ? k : kmin;
+          ++nf;
+        }
+      });
+    }
     flags = block_reduce_max<kBlock, uint32_t>(flags, sh.red32);
     kmax = block_reduce_max<kBlock, uint32_t>(kmax, sh.red32);
     kmin = block_reduce_min<kBlock, uint32_t>(kmin, sh.red32);
