@@ -38,6 +38,7 @@ struct Args {
   float ln_min_p_lo;  // ln(min_p) minus a safety margin: the min-p candidate band
   int S, chunk_len;
   int hash_bits, bitmap_words;
+  int mask_lds;  // masked streamed rows: byte offset of the chunk's allow-mask words in dynamic LDS
   int aligned, write_probs;
   int pen_mono;  // repetition >= 1, frequency >= 0, presence >= 0: a penalty never raises z
   uint32_t* hdr;   // [B*S*2]            count, flags of each chunk list

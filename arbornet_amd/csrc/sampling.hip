@@ -155,6 +155,7 @@ struct Plan {
   int S, chunk_len;
   int hash_bits, bitmap_words;
   size_t lds_stream, lds_solver;
+  int mask_lds;  // byte offset of the LDS mask words (streamed masked rows), else -1
   // workspace layout (byte offsets)
   size_t off_hdr, off_cand, off_zbuf, off_split, off_ctr, total;
 };
@@ -424,7 +425,14 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
     return fail(ARBOR_ERR_MASK, "mask_words %d < ceil(vocab / 32) = %d", p->mask_words, (p->vocab + 31) / 32);
   const bool probs = (p->flags & ARBOR_FLAG_WRITE_PROBS) != 0;
   if (probs && !out_probs) return fail(ARBOR_ERR_FLAGS, "ARBOR_FLAG_WRITE_PROBS without out_probs");
-  const Plan pl = make_plan(p, device_cus());
+  Plan pl = make_plan(p, device_cus());
+  // masked streamed fp32 rows keep the chunk's allow-mask words in LDS (after the history
+  // table), so a unit's mask is known before its logits are requested
+  pl.mask_lds = -1;
+  if (allow_mask && pl.path == Path::Stream && p->dtype == ARBOR_DTYPE_F32) {
+    pl.mask_lds = (int)pl.lds_stream;
+    pl.lds_stream += sizeof(uint32_t) * (size_t)(pl.chunk_len / 32);
+  }
   if (!workspace || workspace_bytes < pl.total)
     return fail(ARBOR_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? workspace_bytes : 0,
                 pl.total);
@@ -455,6 +463,7 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   a.chunk_len = pl.chunk_len;
   a.hash_bits = pl.hash_bits;
   a.bitmap_words = pl.bitmap_words;
+  a.mask_lds = pl.mask_lds;
   const size_t esz = p->dtype == ARBOR_DTYPE_BF16 ? 2 : 4;
   a.aligned = ((uintptr_t)logits % 16 == 0) && (((size_t)p->ld_logits * esz) % 16 == 0);
   a.write_probs = probs ? 1 : 0;

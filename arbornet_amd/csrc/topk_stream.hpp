@@ -149,7 +149,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   // in flight (the compiler otherwise loads them where they are first used).
   __asm__ volatile("" ::"s"(a.logits), "s"(a.ld), "s"(a.V), "s"(a.hist), "s"(a.H), "s"(a.mask), "s"(a.mask_words),
                    "s"(a.uniforms), "s"(a.inv_t), "s"(a.temp), "s"(a.top_k), "s"(a.S), "s"(a.chunk_len),
-                   "s"(a.hash_bits), "s"(a.bitmap_words), "s"(a.write_probs), "s"(a.pen_mono), "s"(a.top_p),
+                   "s"(a.hash_bits), "s"(a.bitmap_words), "s"(a.mask_lds), "s"(a.write_probs), "s"(a.pen_mono), "s"(a.top_p),
                    "s"(a.min_p), "s"(a.out_ids), "s"(a.out_probs));
   constexpr int VEC = Elem<DT>::kVec;
   constexpr int U = TkUnits<DT>::value;
@@ -205,22 +205,43 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   const __amdgpu_buffer_rsrc_t mrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(MASK ? mrow : nullptr), (short)0,
                                         MASK ? a.mask_words * 4 : 0, kBufferWord3);
-  auto load = [&](int bi, Batch& bt) __attribute__((always_inline)) {
+  // Masked fp32 rows: the chunk's mask words are copied to LDS while the first batch is in
+  // flight; every later batch reads a unit's word there first and does not request the
+  // logits of a unit with no allowed id (a masked logit is -inf whatever its value). bf16
+  // rows load each unit's word beside its logits (measured faster for them).
+  constexpr bool SKIP = MASK && DT == ARBOR_DTYPE_F32;
+  const uint32_t* lmask = SKIP ? reinterpret_cast<const uint32_t*>(smem + a.mask_lds) : nullptr;
+  constexpr uint32_t kUnitBits = (1u << VEC) - 1u;
+  constexpr int kPastChunk = 0x7FFFFFF0;  // a buffer offset past every chunk: reads zeros, no access
+  // from_lds: the mask words are in LDS (every batch after the first)
+  auto load = [&](int bi, Batch& bt, bool from_lds) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int unit = bi * kBatch + u * kWave + lane;
+      uint32_t mw = 0u;
+      bool skip = false;
+      if (SKIP && from_lds) {
+        mw = unit < n_units ? lmask[(unit * VEC) >> 5] : 0u;
+        skip = ((mw >> ((unit * VEC) & 31)) & kUnitBits) == 0u;
+      }
       if (ALIGNED) {
-        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, unit * 16, 0, kBufferNt);
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, skip ? kPastChunk : unit * 16, 0, kBufferNt);
         bt.w[u][0] = v.x;
         bt.w[u][1] = v.y;
         bt.w[u][2] = v.z;
         bt.w[u][3] = v.w;
-        if (MASK) bt.mw[u] = __builtin_amdgcn_raw_buffer_load_b32(mrs, ((c0 + unit * VEC) >> 5) * 4, 0, 0);
+        if (MASK && !(SKIP && from_lds)) mw = __builtin_amdgcn_raw_buffer_load_b32(mrs, ((c0 + unit * VEC) >> 5) * 4, 0, 0);
       } else {
         const int e0 = c0 + unit * VEC;
-        load_raw<DT>(xrow, e0, c1, false, bt.w[u]);
-        if (MASK) bt.mw[u] = e0 < c1 ? mrow[e0 >> 5] : 0u;
+        if (skip) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bt.w[u][j] = 0u;
+        } else {
+          load_raw<DT>(xrow, e0, c1, false, bt.w[u]);
+        }
+        if (MASK && !(SKIP && from_lds)) mw = e0 < c1 ? mrow[e0 >> 5] : 0u;
       }
+      if (MASK) bt.mw[u] = mw;
     }
   };
   auto unit_of = [&](int b, int q) { return b * kBatch + (q / VEC) * kWave + lane; };
@@ -273,7 +294,11 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   // loads return as zeros without a memory access
   Batch ba, bb, bc;
   int ia = finisher ? n_batches : wave, ib = wave + kTkStream, ic = wave + 2 * kTkStream;
-  load(ia, ba);
+  load(ia, ba, false);
+  if (SKIP) {
+    uint32_t* lm = reinterpret_cast<uint32_t*>(smem + a.mask_lds);
+    for (int i = t; i < (c1 - c0 + 31) / 32; i += kTkBlock) lm[i] = mrow[(c0 >> 5) + i];
+  }
   if (t == 0) {
     s.flags = 0u;
     s.tmax = 0u;
@@ -439,8 +464,8 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       sample_add(s.hist, order_key(lm + 0.0f));
       wave_lds_sync();
     }
-    load(ib, bb);
-    load(ic, bc);
+    load(ib, bb, true);
+    load(ic, bc, true);
 
     // ---- B. stream ----
     uint64_t* stage = L.stage + wave * kTkStage;
@@ -628,15 +653,15 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       refresh();
       process(ia, ba);
       ia = grab();
-      load(ia, ba);
+      load(ia, ba, true);
       if (ib >= n_batches) break;
       process(ib, bb);
       ib = grab();
-      load(ib, bb);
+      load(ib, bb, true);
       if (ic >= n_batches) break;
       process(ic, bc);
       ic = grab();
-      load(ic, bc);
+      load(ic, bc, true);
     }
 
     // history ids a penalty may raise: the row's first chunk scores all of them
