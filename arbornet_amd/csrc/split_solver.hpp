@@ -39,7 +39,11 @@ struct SplitChunk {
   int32_t ncoll;                    // entries of the selected sub-bin (may exceed kFsColl)
   // one histogram per level: a workgroup writes its level-1 histogram while others of the
   // row may still be reading its level-0 one (the next write to a level's histogram comes
-  // two barriers later, after every reader has passed the barrier between)
+  // two barriers later, after every reader has passed the barrier between); with the
+  // totals of its 64 groups of 64 bins, so that a reader fetches the group totals and then
+  // only the selected group's bins
+  unsigned long long gcnt[2][kFsBins / 64];
+  unsigned long long gmass[2][kFsBins / 64];
   uint32_t cnt[2][kFsBins];
   unsigned long long mass[2][kFsBins];
   unsigned long long coll_key[kFsColl];
@@ -193,6 +197,7 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
     int b0 = 0, b1 = 0;
     bool all = false;     // the whole row is below the target: keep everything
     bool direct = false;  // the level-0 bin is collected whole (no level 1)
+    uint64_t sel_cnt = 0;  // entries of the selected bin
     for (int level = 0; level < 2; ++level) {
       if (!skip && !all) {
         for (int i = t; i < kFsBins; i += kBlock) {
@@ -218,79 +223,71 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
           mine->cnt[level][i] = sh.cnt[i];
           mine->mass[level][i] = sh.mass[i];
         }
+        // group totals (group g = bins [64g, 64g + 64)): wave w sums groups w, w + 16, ...
+#pragma unroll
+        for (int j = 0; j < kFsBins / kBlock; ++j) {
+          const int bin = j * kBlock + t;
+          const uint64_t gc = wave_sum((uint64_t)sh.cnt[bin]);
+          const uint64_t gm = wave_sum((uint64_t)sh.mass[bin]);
+          if (lane == 0) {
+            mine->gcnt[level][bin >> 6] = gc;
+            mine->gmass[level][bin >> 6] = gm;
+          }
+        }
       }
       sync_row();
       if (!skip && !all) {
-        // the row's histogram: the sum of its chunks' (every load of a thread in flight at
-        // once: four bins, four chunks at a time)
-        constexpr int PER = kFsBins / kBlock;
-        uint32_t cn[PER] = {};
-        unsigned long long ms[PER] = {};
-        for (int c0s = 0; c0s < S; c0s += 4) {
-          uint32_t cv[4][PER];
-          unsigned long long mv[4][PER];
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int q = 0; q < PER; ++q) {
-              const int c = c0s + j < S ? c0s + j : c0s;
-              cv[j][q] = rowc[c].cnt[level][t + q * kBlock];
-              mv[j][q] = rowc[c].mass[level][t + q * kBlock];
-            }
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (c0s + j < S)
-#pragma unroll
-              for (int q = 0; q < PER; ++q) {
-                cn[q] += cv[j][q];
-                ms[q] += mv[j][q];
-              }
+        // The row's bin, found by every wave on its own (the same in each: exact integer
+        // sums): the row's 64 group totals (lane g: group g), the group in which the
+        // running weight from the top reaches the target, then that group's 64 bins
+        // (lane l: bin 64g + l) and the bin in which it does, as fs_find_bin finds it
+        // over all 4096 bins. Weights are counts (by_mass false) or masses.
+        uint64_t gc = 0, gm = 0;
+        for (int c = 0; c < S; ++c) {
+          gc += rowc[c].gcnt[level][lane];
+          gm += rowc[c].gmass[level][lane];
         }
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-          sh.cnt[t + q * kBlock] = cn[q];
-          sh.mass[t + q * kBlock] = ms[q];
-        }
-        __syncthreads();
         if (level == 0 && frac > 0.0) {
-          uint64_t m = 0;
-          for (int b = t; b < kFsBins; b += kBlock) m += sh.mass[b];
-          m = fs_sum<kBlock>(m, sh.red64);
+          const uint64_t m = wave_sum(gm);
           const double tg = ceil(frac * (double)m);
           target = tg < 1.0 ? 1ull : (uint64_t)tg;
           if (target > m) target = m;
         }
-        uint64_t above;
-        const int b = fs_find_bin<kBlock>(sh, by_mass, target - above_w, &above);
-        if (b < 0) {
-          all = true;
+        const uint64_t tgt = target - above_w;
+        const uint64_t gw = by_mass ? gm : gc;
+        const uint64_t gin = wave_scan_incl(gw);
+        const uint64_t ghit = __ballot(gin - gw < tgt && gin >= tgt);
+        if (ghit == 0ull) {
+          all = true;  // the whole level is below the target: keep everything
         } else {
-          uint64_t ac = 0, am = 0;
-          for (int j = t; j < kFsBins; j += kBlock)
-            if (j < b) {
-              ac += sh.cnt[j];
-              am += sh.mass[j];
-            }
-          ac = fs_sum<kBlock>(ac, sh.red64);
-          am = fs_sum<kBlock>(am, sh.red64);
-          above_w += above;
-          above_c += ac;
-          above_m += am;
+          const int g = __ffsll((long long)ghit) - 1;
+          const uint64_t gex_c = lane_get(wave_scan_incl(gc) - gc, g);  // groups above g
+          const uint64_t gex_m = lane_get(wave_scan_incl(gm) - gm, g);
+          const uint64_t gex_w = by_mass ? gex_m : gex_c;
+          uint64_t bc = 0, bm = 0;
+          for (int c = 0; c < S; ++c) {
+            bc += rowc[c].cnt[level][g * 64 + lane];
+            bm += rowc[c].mass[level][g * 64 + lane];
+          }
+          const uint64_t bw = by_mass ? bm : bc;
+          const uint64_t bin = gex_w + wave_scan_incl(bw);
+          // the group's bins sum to its total, which reaches the target: one bin does
+          const int l = __ffsll((long long)__ballot(bin - bw < tgt && bin >= tgt)) - 1;
+          above_w += lane_get(bin - bw, l);
+          above_c += gex_c + lane_get(wave_scan_incl(bc) - bc, l);
+          above_m += gex_m + lane_get(wave_scan_incl(bm) - bm, l);
+          sel_cnt = lane_get(bc, l);
           if (level == 0)
-            b0 = b;
+            b0 = g * 64 + l;
           else
-            b1 = b;
+            b1 = g * 64 + l;
         }
       }
       // a level-0 bin small enough to collect whole needs no level 1: every workgroup of the
       // row summed the same counts, so all of them leave here or none
-      if (level == 0 && !skip && !all) {
-        const bool small = sh.cnt[b0] <= (uint32_t)kFsColl;
-        __syncthreads();  // every thread has read the count before level 1 clears the bins
-        if (small) {
-          direct = true;
-          break;
-        }
+      if (level == 0 && !skip && !all && sel_cnt <= (uint64_t)kFsColl) {
+        direct = true;
+        break;
       }
     }
     // the chunk's entries of the selected sub-bin

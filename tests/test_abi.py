@@ -145,7 +145,7 @@ def test_workspace_bytes_configs(name):
     need = S.workspace_bytes(p)
     # at most one fp32 row buffer per row, plus (rows split over workgroups) one ~112 KB
     # record per workgroup, at most one workgroup per compute unit of the largest part
-    assert 0 < need <= w.batch * w.vocab * 4 + (16 << 20) + 256 * (113 << 10) + 4 * w.batch
+    assert 0 < need <= w.batch * w.vocab * 4 + (16 << 20) + 256 * (115 << 10) + 4 * w.batch
     p.flags = S.ARBOR_FLAG_WRITE_PROBS
     assert S.workspace_bytes(p) > 0
 
