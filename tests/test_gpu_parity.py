@@ -281,7 +281,7 @@ def _random_case(i):
     return B, V, ld, dtype, H, mf, kw
 
 
-@pytest.mark.parametrize("i", range(100))
+@pytest.mark.parametrize("i", range(300))
 def test_random_parameter_sets(i):
     B, V, ld, dtype, H, mf, kw = _random_case(i)
     _announce(f"[random {i}] B={B} V={V} ld={ld} {dtype} H={H} mask={mf} {kw}")
