@@ -60,13 +60,16 @@ constexpr int kBufferWord3 = 0x00020000;    // buffer resource word 3 (gfx9 fami
 constexpr int kBufferNt = 2;                // buffer load cache policy: non-temporal
 static_assert((kTkQueue & (kTkQueue - 1)) == 0, "the ring size is a power of two");
 
-// 16-byte loads per lane per batch (three batches per lane in flight or in hand)
+// 16-byte loads per lane per batch (three batches per lane in flight or in hand), chosen
+// by measurement: fp32 2; bf16 3 (min-p band rows of 152K ids: 39.8 us per 512 rows
+// against 50.1 with 2 and 43.1 with 1; 4 spills); masked bf16 rows 2 (3 measured slower),
+// and unaligned bf16 rows 2 (3 spills there)
 #ifndef TK_UNITS_F32
 #define TK_UNITS_F32 2
 #endif
-template <int DT>
+template <int DT, bool MASK, bool ALIGNED>
 struct TkUnits {
-  static constexpr int value = DT == ARBOR_DTYPE_F32 ? TK_UNITS_F32 : 2;
+  static constexpr int value = DT == ARBOR_DTYPE_F32 ? TK_UNITS_F32 : (MASK || !ALIGNED ? 2 : 3);
 };
 
 // Counts of the sample's lane-maximum keys by their top 12 bits, with a 64-bin summary
@@ -152,7 +155,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
                    "s"(a.hash_bits), "s"(a.bitmap_words), "s"(a.mask_lds), "s"(a.write_probs), "s"(a.pen_mono), "s"(a.top_p),
                    "s"(a.min_p), "s"(a.out_ids), "s"(a.out_probs));
   constexpr int VEC = Elem<DT>::kVec;
-  constexpr int U = TkUnits<DT>::value;
+  constexpr int U = TkUnits<DT, MASK, ALIGNED>::value;
   constexpr int NQ = VEC * U;        // elements per lane per batch
   constexpr int kBatch = U * kWave;  // units per batch
   constexpr int HIDR = ARBOR_HISTORY_MAX / (kTkStream * kWave) + 1;  // history ids per streaming lane
