@@ -197,10 +197,13 @@ __device__ __forceinline__ void fs_temper_stats(const Args& a, const void* xrow,
 // Level-0 bin of d = zmax - v (scale = kFsBins / span), and the level-1 sub-bin of an
 // entry of level-0 bin b0. Non-decreasing in d, i.e. bins ascend as the rank descends.
 __device__ __forceinline__ float fs_x(float v, float zmax, float scale) { return (zmax - v) * scale; }
-__device__ __forceinline__ int fs_bin0(float x) { return x >= (float)(kFsBins - 1) ? kFsBins - 1 : (int)x; }
+// Bin indices are clamped to [0, kFsBins) whatever x is (NaN reads as 0).
+__device__ __forceinline__ int fs_bin0(float x) {
+  return x >= (float)(kFsBins - 1) ? kFsBins - 1 : (int)fmaxf(x, 0.0f);
+}
 __device__ __forceinline__ int fs_bin1(float x, int b0) {
   const float y = (x - (float)b0) * (float)kFsBins;
-  return y >= (float)(kFsBins - 1) ? kFsBins - 1 : (int)y;
+  return y >= (float)(kFsBins - 1) ? kFsBins - 1 : (int)fmaxf(y, 0.0f);
 }
 
 // The bin (in ascending bin order, i.e. descending rank) at which the running weight of bins, from the top,

@@ -19,8 +19,10 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <cmath>
 #include <mutex>
 
@@ -189,17 +191,18 @@ int validate(const arbor_sampling_params* p) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Compute units of the current device (cached per device; 256 on MI355X).
+// Compute units of the current device (256 on MI355X), cached per device. Concurrent
+// first calls may both query the device; they store the same value atomically.
 int device_cus() {
-  static int cache[64];
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] <= 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 Plan make_plan(const arbor_sampling_params* p, int cus) {
@@ -255,7 +258,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   if (pl.path == Path::Solver && pl.S > 1) {
     off = align_up(off + sizeof(arbor::SplitChunk) * (size_t)B * (size_t)pl.S, 256);
     pl.off_ctr = off;
-    off = align_up(off + sizeof(uint32_t) * ((size_t)B + 1), 256);  // row barriers + ticket
+    off = align_up(off + sizeof(uint32_t) * (2 * (size_t)B + 1), 256);  // row barriers, ticket, failure words
   }
   pl.total = off;
   return pl;
@@ -357,6 +360,18 @@ bool split_fits(const void* kernel, size_t lds, int blocks) {
   return total >= blocks;
 }
 
+// Spin limit of the split solver's row barriers: kSplitSpinLimit (seconds of waiting), or
+// ARBOR_SPLIT_SPIN_LIMIT from the environment. Tests set a tiny limit to exercise the
+// give-up path (every kernel still ends: a wait that gives up stops waiting).
+uint32_t split_spin_limit() {
+  const char* env = getenv("ARBOR_SPLIT_SPIN_LIMIT");
+  if (env && *env) {
+    const unsigned long v = strtoul(env, nullptr, 10);
+    if (v > 0 && v < arbor::kSplitSpinLimit) return (uint32_t)v;
+  }
+  return arbor::kSplitSpinLimit;
+}
+
 // The row solver: S workgroups per row when the plan splits rows and the grid can be
 // resident at once, else one workgroup per row.
 template <int DT>
@@ -371,14 +386,14 @@ int launch_solver(const Plan& pl, hipStream_t st, arbor::Args a, char* ws) {
     if (split_fits(split, lds, a.B * pl.S)) {
       arbor::SplitChunk* chunks = reinterpret_cast<arbor::SplitChunk*>(ws + pl.off_split);
       uint32_t* ctr = reinterpret_cast<uint32_t*>(ws + pl.off_ctr);
-      // the rows' barrier counters and the ticket counter start at zero (a fill kernel: no
-      // memset node in a captured graph)
-      hipLaunchKernelGGL(arbor::zero_u32_kernel, dim3((unsigned)((a.B + 1 + 255) / 256)), dim3(256), 0, st, ctr,
-                         a.B + 1);
+      // the rows' barrier counters, the ticket counter and the rows' failure words start at
+      // zero (a fill kernel: no memset node in a captured graph)
+      const int nctr = 2 * a.B + 1;
+      hipLaunchKernelGGL(arbor::zero_u32_kernel, dim3((unsigned)((nctr + 255) / 256)), dim3(256), 0, st, ctr, nctr);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return hip_fail(e, "kernel launch");
       hipLaunchKernelGGL(arbor::split_solver_kernel<DT>, dim3((unsigned)(a.B * pl.S)), dim3(arbor::kBlock), lds, st, a,
-                         chunks, ctr);
+                         chunks, ctr, split_spin_limit());
       e = hipGetLastError();
       if (e != hipSuccess) return hip_fail(e, "kernel launch");
       return ARBOR_OK;

@@ -53,30 +53,54 @@ struct SplitChunk {
 constexpr uint32_t kSplitSpinLimit = 1u << 26;  // seconds of waiting: a barrier that never fills is a bug
 
 // Barrier of the workgroups of one row. *ctr counts arrivals over the whole call (zeroed
-// before the launch, like the ticket counter); the n-th barrier of a row waits for n * S arrivals. Global writes
-// made before it are visible to the row's other workgroups after it (agent-scope release
-// before the arrival, acquire after the wait). A wait past the spin limit gives up and
-// sets *timed_out instead of hanging.
-__device__ __forceinline__ void row_barrier(uint32_t* ctr, uint32_t target, int* timed_out) {
+// before the launch, like the ticket counter and the row's failure word *fail); the n-th
+// barrier of a row waits for n * S arrivals. Global writes made before it are visible to
+// the row's other workgroups after it (agent-scope release before the arrival, acquire
+// after the wait).
+// A wait past `spin_limit` gives up: it sets the row's failure word (before any later
+// arrival of this workgroup, so every workgroup that counts such an arrival sees it) and
+// *timed_out. A workgroup that has timed out, or has seen the failure word, still arrives
+// at every later barrier (so the counts stay whole) but waits at none and computes nothing
+// more; the row's result is then ARBOR_ID_STALLED.
+__device__ __forceinline__ void row_barrier(uint32_t* ctr, uint32_t* fail, uint32_t target, uint32_t spin_limit,
+                                            int* timed_out) {
   __syncthreads();
   if (threadIdx.x == 0) {
     __threadfence();
     atomicAdd(ctr, 1u);
-    uint32_t spins = 0u;
-    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++spins == kSplitSpinLimit) {
-        *timed_out = 1;
-        break;
+    if (!*timed_out) {
+      uint32_t spins = 0u;
+      while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        if (__hip_atomic_load(fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins >= spin_limit) {
+          __hip_atomic_store(fail, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
       }
+      __threadfence();
+      if (__hip_atomic_load(fail, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) *timed_out = 1;
     }
-    __threadfence();
   }
   __syncthreads();
 }
 
+// The row's id, written once every workgroup of the row is past its last barrier: a
+// workgroup that timed out stores ARBOR_ID_STALLED unconditionally; the one that found the
+// draw stores its id only if no ARBOR_ID_STALLED is there, so the sentinel wins whichever
+// store comes first.
+__device__ __forceinline__ void store_row_id(int32_t* out, int32_t id) {
+  int32_t cur = __hip_atomic_load(out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (cur != ARBOR_ID_STALLED) {
+    if (__hip_atomic_compare_exchange_strong(out, &cur, id, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      break;
+  }
+}
+
 template <int DT>
-__global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk* chunks, uint32_t* ctr) {
+__global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk* chunks, uint32_t* ctr,
+                                                               uint32_t spin_limit) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint32_t* htab = reinterpret_cast<uint32_t*>(smem);
   FastShared& sh = *reinterpret_cast<FastShared*>(smem + ((sizeof(uint32_t) << a.hash_bits) + 15) / 16 * 16);
@@ -84,7 +108,8 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
   __shared__ uint32_t s_ticket;
   constexpr int NW = kWaves;
   const int t = threadIdx.x, lane = lane_id(), wave = t / kWave;
-  // (row, chunk) in start order: ctr[B] is the ticket counter, ctr[0..B) the row barriers
+  // (row, chunk) in start order: ctr[B] is the ticket counter, ctr[0..B) the row barriers,
+  // ctr[B + 1 + row] the rows' failure words
   if (t == 0) s_ticket = atomicAdd(ctr + a.B, 1u);
   __syncthreads();
   const int ticket = (int)s_ticket;
@@ -101,7 +126,12 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
   float* prow = a.write_probs ? a.out_probs + (size_t)row * (size_t)V : nullptr;
   uint32_t passed = 0u;  // row barriers passed
   if (t == 0) s_timeout = 0;
-  auto sync_row = [&]() { row_barrier(ctr + row, ++passed * (uint32_t)S, &s_timeout); };
+  uint32_t* fail_w = ctr + a.B + 1 + row;
+  bool skip = false;  // this workgroup has nothing more to compute (it still meets every barrier)
+  auto sync_row = [&]() {
+    row_barrier(ctr + row, fail_w, ++passed * (uint32_t)S, spin_limit, &s_timeout);
+    if (s_timeout) skip = true;
+  };
 
   // ---- 1. history table, the chunk's z, its statistics ----
   uint32_t flags = 0u;
@@ -177,11 +207,11 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
     nf += rowc[c].nf;
     rflags |= rowc[c].flags;
   }
-  bool skip = false;  // this workgroup has nothing more to compute (it still meets every barrier)
-  if (rflags != 0u || nf == 0u) {
+  if (!skip && (rflags != 0u || nf == 0u)) {
     if (chunk == 0 && t == 0)
-      a.out_ids[row] = (rflags & kFlagBadHistory) ? ARBOR_ID_BAD_HISTORY
-                                                   : ((rflags & kFlagInvalid) ? ARBOR_ID_INVALID : ARBOR_ID_EMPTY);
+      store_row_id(a.out_ids + row, (rflags & kFlagBadHistory)
+                                        ? ARBOR_ID_BAD_HISTORY
+                                        : ((rflags & kFlagInvalid) ? ARBOR_ID_INVALID : ARBOR_ID_EMPTY));
     if (prow)
       for (int i = c0 + t; i < c1; i += kBlock) prow[i] = 0.0f;
     skip = true;
@@ -441,7 +471,11 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
     }
   }
   sync_row();
-  if (skip) return;
+  if (skip) {
+    if (s_timeout && t == 0) __hip_atomic_exchange(a.out_ids + row, ARBOR_ID_STALLED, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   uint64_t E = 0, before = 0;
   int32_t last = -1;
   for (int c = 0; c < S; ++c) {
@@ -489,11 +523,10 @@ __global__ void __launch_bounds__(kBlock) split_solver_kernel(Args a, SplitChunk
       }
     }
     __syncthreads();
-    if (t == 0) a.out_ids[row] = sh.b32[3] >= 0 ? sh.b32[3] : last;
+    if (t == 0) store_row_id(a.out_ids + row, sh.b32[3] >= 0 ? sh.b32[3] : last);
   } else if (target >= E && last >= c0 && last < c1) {
-    if (t == 0) a.out_ids[row] = last;  // no crossing (u * E rounds to E or u is NaN): the last kept id
+    if (t == 0) store_row_id(a.out_ids + row, last);  // no crossing (u * E rounds to E, or NaN u): the last kept id
   }
-  if (s_timeout && t == 0) a.out_ids[row] = ARBOR_ID_INVALID;  // a barrier gave up: never expected
   if (prow) {
     const double Ed = (double)E / (double)kMassScale;
     fs_visit<kBlock>(zc, n, [&](int i, float v) {

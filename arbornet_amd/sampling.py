@@ -30,6 +30,7 @@ ARBOR_FLAG_WRITE_PROBS = 1
 ARBOR_ID_EMPTY = -1
 ARBOR_ID_INVALID = -2
 ARBOR_ID_BAD_HISTORY = -3
+ARBOR_ID_STALLED = -4
 
 STATUS_NAMES = {
     0: "ARBOR_OK",
@@ -80,17 +81,24 @@ class SamplingParams(ctypes.Structure):
         ("flags", ctypes.c_uint32),
     ]
 
+    # integer fields whose C type is int32_t: ctypes would wrap larger values silently
+    _INT32_FIELDS = ("batch", "vocab", "ld_logits", "dtype", "top_k", "hist_len", "mask_words")
+
     @classmethod
     def make(cls, batch: int, vocab: int, **kw) -> "SamplingParams":
+        """Params with the library's defaults, overridden by ``kw``. Integer fields must fit
+        int32: a row stride of 2^31 elements or more (e.g. ``ld_logits = seq * vocab`` of a
+        long [batch, seq, vocab] output) raises ARBOR_ERR_SHAPE instead of wrapping."""
+        vals = dict(batch=batch, vocab=vocab, ld_logits=vocab, dtype=ARBOR_DTYPE_F32, temperature=1.0,
+                    repetition_penalty=1.0, top_p=1.0, mask_words=(vocab + 31) // 32)
+        vals.update(kw)
         p = cls()
         p.struct_size = ctypes.sizeof(cls)
-        p.batch, p.vocab, p.ld_logits = batch, vocab, vocab
-        p.dtype = ARBOR_DTYPE_F32
-        p.temperature, p.repetition_penalty, p.top_p = 1.0, 1.0, 1.0
-        p.mask_words = (vocab + 31) // 32
-        for k, v in kw.items():
+        for k, v in vals.items():
             if not hasattr(p, k):
                 raise AttributeError(k)
+            if k in cls._INT32_FIELDS and not (-2**31 <= int(v) < 2**31):
+                raise ArborSamplingError(-3, f"{k} = {int(v)} does not fit int32 (the ABI field is int32_t)")
             setattr(p, k, v)
         return p
 
@@ -174,14 +182,19 @@ def sample_append_raw(params: SamplingParams, logits: int, history: int, positio
 _workspaces: dict = {}
 
 
-def _workspace(device, nbytes: int):
-    """A workspace of at least nbytes on `device`, cached per device (calls on one device
-    are ordered on torch's current stream, so they may share it)."""
+def _workspace(device, stream: int, nbytes: int):
+    """A workspace of at least nbytes on `device` for calls launched on `stream` (a raw
+    stream handle), cached per (device, stream). Calls that share a workspace must be
+    ordered, and calls on one stream are; calls on different streams get different
+    buffers. A buffer is allocated while its stream is torch's current stream, so the
+    caching allocator hands its memory, once replaced and freed, only to later work on
+    that same stream."""
     import torch
 
-    key = (device.type, device.index)
+    key = (device.type, device.index, int(stream or 0))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        _workspaces.pop(key, None)
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
@@ -242,8 +255,8 @@ class Sampling:
         need = workspace_bytes(p)
         if need == 0:  # invalid params: let arbor_sample report why
             need = 256
-        ws = _workspace(dev, need)
         stream = torch.cuda.current_stream(dev).cuda_stream
+        ws = _workspace(dev, stream, need)
         check(sample_raw(p, logits.data_ptr(), hist_ptr, mask_ptr, uniforms.data_ptr(), out_ids.data_ptr(),
                          probs_ptr, ws.data_ptr(), ws.numel(), stream))
         return (out_ids, out_probs) if write_probs else out_ids
@@ -313,8 +326,8 @@ class GenerationState:
         if out_ids is None:
             out_ids = torch.empty(self.batch, dtype=torch.int32, device=self.device)
         need = workspace_bytes(p) or 256
-        ws = _workspace(self.device, need)
         stream = torch.cuda.current_stream(self.device).cuda_stream
+        ws = _workspace(self.device, stream, need)
         check(sample_append_raw(p, logits.data_ptr(), self.history.data_ptr(), self.positions.data_ptr(), mask_ptr,
                                 uniforms.data_ptr(), out_ids.data_ptr(), None, ws.data_ptr(), ws.numel(), stream))
         return out_ids

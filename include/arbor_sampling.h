@@ -12,7 +12,10 @@
  * DEVICE pointer. The caller owns all memory, as with the reference's CUDA DLL, whose
  * kernels never allocate (ArborNet.Core/Backends/CudaBackend.cs:43-46 allocates,
  * :437-449 frees). Calls are asynchronous and stream-ordered; stream NULL is the
- * default stream. The library keeps no global state and takes no locks.
+ * default stream. Nothing of one call outlives it: no per-call state is kept between
+ * calls. The library does cache facts about each device it has seen (compute-unit count,
+ * kernels' LDS limits and occupancy), filled on first use behind a mutex or atomics, so
+ * concurrent calls from several host threads are safe.
  *
  * Status convention: 0 = success, negative = argument error (ARBOR_ERR_*, checked on the
  * host before anything is launched), positive = HIP runtime error code. The message of
@@ -69,6 +72,8 @@ extern "C" {
 #define ARBOR_ID_EMPTY (-1)          /* no finite tempered logit survives (all masked or -inf) */
 #define ARBOR_ID_INVALID (-2)        /* a tempered, penalised, unmasked logit is NaN or +inf */
 #define ARBOR_ID_BAD_HISTORY (-3)    /* the row's history holds an id >= vocab */
+#define ARBOR_ID_STALLED (-4)        /* a wait between the workgroups that share the row gave up
+                                        after seconds (never expected: report it as a bug) */
 
 /*
  * Sampling parameters. A host POD passed by pointer; struct_size must equal
@@ -79,7 +84,7 @@ typedef struct arbor_sampling_params {
   uint32_t struct_size;
   int32_t batch;               /* rows */
   int32_t vocab;               /* columns sampled per row */
-  int32_t ld_logits;           /* elements between row starts, >= vocab */
+  int32_t ld_logits;           /* elements between row starts, >= vocab and < 2^31 */
   int32_t dtype;               /* ARBOR_DTYPE_F32 or ARBOR_DTYPE_BF16 */
   float temperature;           /* z = x * (1/temperature) in fp32 */
   float repetition_penalty;    /* z > 0 ? z * (1/rp) : z * rp, once per distinct history id */
@@ -119,8 +124,10 @@ int arbor_sample(const arbor_sampling_params* params, const void* logits,
  * One generation step: arbor_sample, then each row's sampled id is appended to the row's
  * device history ring, so that the next step's penalties count it.
  *   logits      the last position of the model's [batch, seq, vocab] output: pass a
- *               pointer to position seq - 1 of row 0 and ld_logits = seq * vocab (or the
- *               [batch, ld_logits] logits of a model that emits one position)
+ *               pointer to position seq - 1 of row 0 and ld_logits = seq * vocab, which
+ *               must stay below 2^31 (seq < 16744 at vocab 128256; copy the last position
+ *               to a [batch, vocab] buffer for longer sequences), or the
+ *               [batch, ld_logits] logits of a model that emits one position
  *   history     [batch, hist_len] int32 ring (device; -1 = empty slot); hist_len > 0
  *   positions   [batch] int32 (device): ids appended to each row so far; the sampled id
  *               goes to slot positions[b] mod hist_len and positions[b] advances. Rows

@@ -61,9 +61,40 @@ def run_gpu(params: S.SamplingParams, inp: syn.Inputs, write_probs: bool = False
     return outs[0], (probs.cpu().numpy() if write_probs else None)
 
 
-def compare(params, inp: syn.Inputs, ids_gpu, probs_gpu=None, label="", fp_rtol=1e-5):
-    """Assert GPU ids equal the oracle's on every non-boundary row; probs within fp_rtol
-    where the kept sets agree. Returns (n_rows, n_boundary, n_boundary_mismatch)."""
+BOUNDARY_TOL = 1e-6  # the oracle's BOUNDARY_TOL: |C_j - u| below this flags a boundary row
+
+
+def check_boundary_row(params, inp: syn.Inputs, r: int, gid: int, oid: int, flip_mass: float, label=""):
+    """A boundary row's GPU id must still be a legitimate draw: a kept id (or, when the
+    top-p / min-p membership of some ids is ambiguous, an id at the edge of the kept set)
+    whose CDF step in ascending id order brackets u to within BOUNDARY_TOL plus the
+    ambiguous mass, and, when no membership is ambiguous, the oracle's id or its immediate
+    neighbour in ascending kept-id order."""
+    _, _, pr = oracle.sample(params, inp.logits, inp.history, inp.mask, inp.uniforms, row0=r, nrows=1, probs=True)
+    q = pr[0].astype(np.float64)
+    kept = np.nonzero(q > 0)[0]
+    u = float(inp.uniforms[r])
+    tol = BOUNDARY_TOL + flip_mass + 1e-7  # + fp32 rounding of the oracle's q
+    assert gid >= 0, f"{label}: boundary row {r}: gpu gave sentinel {gid}, oracle {oid}"
+    before = float(q[kept[kept < gid]].sum())
+    step = float(q[gid]) if gid < q.size else 0.0
+    ok_cdf = before - tol <= u <= before + step + tol
+    assert ok_cdf, (f"{label}: boundary row {r}: gpu id {gid} spans CDF [{before:.9f}, {before + step:.9f}] "
+                    f"which misses u = {u:.9f} by more than {tol:.2e} (oracle id {oid})")
+    if flip_mass == 0.0:
+        pg, po = np.searchsorted(kept, gid), np.searchsorted(kept, oid)
+        assert pg < kept.size and kept[pg] == gid, f"{label}: boundary row {r}: gpu id {gid} is not kept"
+        assert abs(int(pg) - int(po)) <= 1, (f"{label}: boundary row {r}: gpu id {gid} is {int(pg) - int(po)} "
+                                              f"kept places from the oracle's {oid}")
+
+
+def compare(params, inp: syn.Inputs, ids_gpu, probs_gpu=None, label="", fp_rtol=1e-5, max_boundary=None):
+    """Assert GPU ids equal the oracle's on every non-boundary row, and that every boundary
+    row's id passes check_boundary_row; probs within fp_rtol where the kept sets agree.
+    max_boundary bounds the number of boundary rows (default: half the rows, at least 2, so
+    that no test excuses most of its rows; top-p rows that keep tens of thousands of ids
+    have CDF steps of ~1e-5, so a tenth to a third of such rows fall within 1e-6 of one).
+    Returns (n_rows, n_boundary, n_boundary_mismatch)."""
     want_probs = probs_gpu is not None
     ids_o, info, probs_o = oracle.sample(params, inp.logits, inp.history, inp.mask, inp.uniforms,
                                          probs=want_probs, threads=ORACLE_THREADS)
@@ -75,6 +106,11 @@ def compare(params, inp: syn.Inputs, ids_gpu, probs_gpu=None, label="", fp_rtol=
                   for r in rows]
         raise AssertionError(f"{label}: {int(bad.sum())} non-boundary rows differ "
                              f"(row, gpu, oracle, kept, gap): {detail}")
+    n_rows = len(ids_o)
+    limit = max(2, n_rows // 2) if max_boundary is None else max_boundary
+    assert int(boundary.sum()) <= limit, f"{label}: {int(boundary.sum())} boundary rows, more than {limit}"
+    for r in np.nonzero(boundary & (ids_gpu != ids_o))[0]:
+        check_boundary_row(params, inp, int(r), int(ids_gpu[r]), int(ids_o[r]), float(info["flip_mass"][r]), label)
     if want_probs:
         clean = info["flip_mass"] == 0.0
         for r in np.nonzero(clean)[0]:

@@ -44,8 +44,8 @@ def test_abi_version_and_constants():
     assert d["ARBOR_FLAG_WRITE_PROBS"] == S.ARBOR_FLAG_WRITE_PROBS
     for code, name in S.STATUS_NAMES.items():
         assert d[name] == code, name
-    assert (d["ARBOR_ID_EMPTY"], d["ARBOR_ID_INVALID"], d["ARBOR_ID_BAD_HISTORY"]) == (
-        S.ARBOR_ID_EMPTY, S.ARBOR_ID_INVALID, S.ARBOR_ID_BAD_HISTORY)
+    assert (d["ARBOR_ID_EMPTY"], d["ARBOR_ID_INVALID"], d["ARBOR_ID_BAD_HISTORY"], d["ARBOR_ID_STALLED"]) == (
+        S.ARBOR_ID_EMPTY, S.ARBOR_ID_INVALID, S.ARBOR_ID_BAD_HISTORY, S.ARBOR_ID_STALLED)
 
 
 def test_params_layout_matches_c(tmp_path):

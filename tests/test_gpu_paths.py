@@ -1,0 +1,78 @@
+"""GPU parity on the product paths that only large shapes reach: full-vocabulary rows on
+the one-workgroup-per-row solver (a batch that fills the chip), rows longer than 262,144
+ids (the solvers' unfused passes), and rows at the header's vocabulary limit (the streaming
+kernel's forced split into chunks). Each case names the path make_plan takes for it; ids
+must equal the oracle's on every non-boundary row, and boundary rows must pass
+check_boundary_row."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from arbornet_amd import sampling as S
+from arbornet_amd import synthetic as syn
+
+from gpu_helpers import compare, run_gpu
+
+pytestmark = pytest.mark.gpu
+
+# c2's input distribution (N(0, 1.5^2) plus 16 spikes at +6..+12) at other shapes
+BASE = syn.CONFIGS["c2"]
+
+CASES = [
+    # (label, batch, vocab, dtype, sampling overrides, rows whose probabilities are checked)
+    # a batch that fills the chip: one workgroup per row on full-vocabulary rows
+    ("top-p 0.9, B=256 (c2 parameters at c3's batch)", 256, 128256, "f32", {}, 8),
+    ("no filter, B=256", 256, 128256, "f32", dict(top_p=1.0, repetition_penalty=1.0, hist_len=0), 8),
+    ("top-k 300, B=256", 256, 128256, "f32", dict(top_k=300, top_p=1.0), 8),
+    # rows longer than 262,144 ids
+    ("top-k 50 stream, V=300007", 2, 300007, "f32", dict(top_k=50, top_p=1.0), 2),
+    ("top-k 50 stream, V=300007 bf16", 2, 300007, "bf16", dict(top_k=50, top_p=1.0), 2),
+    ("min-p band, V=300007", 2, 300007, "f32", dict(top_p=1.0, min_p=0.05), 2),
+    ("min-p band, V=300007 bf16", 2, 300007, "bf16", dict(top_p=1.0, min_p=0.05), 2),
+    ("top-p split rows, V=300007", 2, 300007, "f32", dict(top_p=0.9), 2),
+    ("top-p split rows, V=300007 bf16", 2, 300007, "bf16", dict(top_p=0.9), 2),
+    ("top-p one row per workgroup, V=300007, B=256", 256, 300007, "f32", dict(top_p=0.9), 4),
+    ("top-p one row per workgroup, V=300007, B=256 bf16", 256, 300007, "bf16", dict(top_p=0.9), 4),
+    ("top-p two chunks of 300,000 ids, B=100", 100, 600000, "f32", dict(top_p=0.9, hist_len=128), 2),
+    # the vocabulary limit: a batch that fills the chip forces the streaming kernel to split
+    # each row into chunks (the chunk's history bitmap holds at most 262,144 ids)
+    ("top-k 50 stream at ARBOR_VOCAB_MAX, B=256 bf16", 256, 1048575, "bf16", dict(top_k=50, top_p=0.95), 2),
+    ("top-k 50 stream at ARBOR_VOCAB_MAX, B=2", 2, 1048575, "f32", dict(top_k=50), 2),
+]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    S.library()
+    yield
+
+
+@pytest.mark.parametrize("case", range(len(CASES)), ids=lambda i: CASES[i][0])
+def test_large_shape_paths(case):
+    label, B, V, dtype, kw, nprob = CASES[case]
+    w = BASE.scaled(batch=B, vocab=V, dtype=dtype, seed=40 + case, **kw)
+    print(f"[paths {case}] {label}: B={B} V={V} {dtype} {kw}", flush=True)
+    sys.stdout.flush()
+    inp = syn.generate(w)
+    ids, _ = run_gpu(S.params_for(w), inp, repeat=2)
+    n, nb, nbm = compare(S.params_for(w), inp, ids, label=label)
+    print(f"[paths {case}] rows {n}, boundary {nb}, boundary rows differing {nbm}", flush=True)
+    if B * V <= 80_000_000:  # probabilities of the whole batch, on the same path
+        ids_p, probs = run_gpu(S.params_for(w), inp, write_probs=True)
+        compare(S.params_for(w), inp, ids_p, probs, label=f"{label} (probs)")
+        assert np.all(ids >= 0)
+        return
+    # probabilities on the first rows only (host copies of a whole batch would be large)
+    ws = w.scaled(batch=nprob)
+    sub = syn.Inputs(inp.logits[:nprob], None if inp.history is None else inp.history[:nprob],
+                     None if inp.mask is None else inp.mask[:nprob], inp.uniforms[:nprob])
+    ids_p, probs = run_gpu(S.params_for(ws), sub, write_probs=True)
+    compare(S.params_for(ws), sub, ids_p, probs, label=f"{label} (probs)")
+    assert np.all(ids >= 0)
