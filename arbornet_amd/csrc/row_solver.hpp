@@ -1,11 +1,12 @@
-// row_solver.hpp -- the exact general path: one workgroup solves one row.
+// row_solver.hpp -- the exact fallback: one workgroup solves one row.
 //
-// z is materialised in the workspace; each cut (top-k by count, top-p by probability
-// mass) is found by an MSB-first radix select on the 64-bit rank key (z descending, id
-// ascending); the draw is a block scan in id order. Mass is fixed point (2^-40), so
-// every sum is exact and independent of reduction order. Used for top-p without top-k,
-// plain sampling, top-k above the streaming limit, and as the fallback of a streamed
-// row whose candidate list overflowed.
+// z is recomputed from the logits on every pass (tempered, masked, penalised from the
+// LDS history table), so the solver needs no workspace; each cut (top-k by count, top-p by
+// probability mass) is found by an MSB-first radix select on the 64-bit rank key (z
+// descending, id ascending); the draw is a block scan in id order. Mass is fixed point
+// (2^-40), so every sum is exact and independent of reduction order. Used for rows with
+// more tied entries at a cut than the histogram solvers rank directly, and for streamed
+// rows whose candidate list could not hold the answer.
 #pragma once
 
 #include "args.hpp"
@@ -45,8 +46,8 @@ struct CutResult {
 // Radix select on the 64-bit rank key over z[0, V): the first element (in rank order)
 // at which the running weight reaches `target` (weight 1 if !by_mass, else fixed-point
 // mass). If frac > 0 the target is ceil(frac * total weight) of the first round.
-template <int BLOCK>
-__device__ CutResult radix_cut(const float* z, int V, float zmax, bool by_mass, uint64_t target,
+template <int BLOCK, typename ZAt>
+__device__ CutResult radix_cut(ZAt zat, int V, float zmax, bool by_mass, uint64_t target,
                                double frac, uint32_t key_hi, uint32_t key_lo, SolverShared& sh) {
   const int t = threadIdx.x;
   const uint64_t chi = (uint64_t)key_hi << 32 | 0xFFFFFFFFull;
@@ -64,7 +65,7 @@ __device__ CutResult radix_cut(const float* z, int V, float zmax, bool by_mass, 
     }
     __syncthreads();
     for (int i = t; i < V; i += BLOCK) {
-      const float v = z[i];
+      const float v = zat(i);
       if (v == -INFINITY) continue;
       const uint64_t c = composite(v, i);
       if ((c & pmask) != prefix) continue;
@@ -126,12 +127,11 @@ __device__ CutResult radix_cut(const float* z, int V, float zmax, bool by_mass, 
 }
 
 // The full contract for one row, by one workgroup of BLOCK threads. htab has
-// 1 << a.hash_bits slots of LDS.
+// 1 << a.hash_bits slots of LDS (when the row has a history).
 template <int BLOCK, int DT>
 __device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab, SolverShared& sh) {
   const int t = threadIdx.x;
   const int V = a.V;
-  float* z = a.zbuf + (size_t)row * (size_t)a.ldz;
   const void* xrow = row_ptr<DT>(a, row);
   const uint32_t* mrow = a.mask ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
   const int P = 1 << a.hash_bits;
@@ -151,27 +151,23 @@ __device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab
         hist_insert(htab, (uint32_t)a.hash_bits, (uint32_t)id);
     }
   }
-  // 2. tempered, masked logits
-  for (int i = t; i < V; i += BLOCK) {
-    float v = Elem<DT>::one(xrow, i) * a.inv_t + 0.0f;
-    if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) v = -INFINITY;
-    z[i] = v;
-  }
-  __syncthreads();
-  // 3. penalties, one writer per distinct history id
-  if (a.H > 0) {
-    for (int s = t; s < P; s += BLOCK) {
-      const uint32_t e = htab[s];
-      if (e == kEmptySlot) continue;
-      const uint32_t id = e >> 12;
-      z[id] = penalize(z[id], (e & 4095u) + 1u, a.pen);
+  __syncthreads();  // the history table is complete
+  // 2. z of id i, recomputed from the logits on every pass: tempered, masked (-inf), and
+  // penalised when i is a history id (the table probe ends at the first empty slot)
+  const bool hist = a.H > 0;
+  auto zat = [&](int i) -> float {
+    if (mrow && !((mrow[i >> 5] >> (i & 31)) & 1u)) return -INFINITY;
+    const float v = Elem<DT>::one(xrow, i) * a.inv_t + 0.0f;
+    if (hist) {
+      const uint32_t c = hist_count(htab, (uint32_t)a.hash_bits, (uint32_t)i);
+      if (c) return penalize(v, c, a.pen);
     }
-  }
-  __syncthreads();
-  // 4. row statistics
+    return v;
+  };
+  // 3. row statistics
   uint32_t kmax = 0, kmin = 0xFFFFFFFFu, nf = 0;
   for (int i = t; i < V; i += BLOCK) {
-    const float v = z[i];
+    const float v = zat(i);
     if (is_invalid(v)) flags |= kFlagInvalid;
     if (v != -INFINITY && !is_invalid(v)) {
       const uint32_t k = order_key(v);
@@ -197,7 +193,7 @@ __device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab
   // 5. cuts: top-k (count), then top-p (mass of the top-k survivors)
   uint64_t cut = 0ull;
   if (a.top_k > 0 && (uint32_t)a.top_k < nf) {
-    const CutResult ck = radix_cut<BLOCK>(z, V, zmax, false, (uint64_t)a.top_k, 0.0, kmax, kmin, sh);
+    const CutResult ck = radix_cut<BLOCK>(zat, V, zmax, false, (uint64_t)a.top_k, 0.0, kmax, kmin, sh);
     cut = ck.cut;
   }
   if (a.top_p < 1.0f) {
@@ -206,16 +202,16 @@ __device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab
       // mass of the top-k survivors
       uint64_t m = 0;
       for (int i = t; i < V; i += BLOCK) {
-        const float v = z[i];
+        const float v = zat(i);
         if (v != -INFINITY && composite(v, i) >= cut) m += mass_fixed(rel_exp(v, zmax));
       }
       m = block_reduce_sum<BLOCK, uint64_t>(m, sh.red64);
       const double tg = ceil((double)a.top_p * (double)m);
       uint64_t target = tg < 1.0 ? 1ull : (uint64_t)tg;
       if (target > m) target = m;
-      cp = radix_cut<BLOCK>(z, V, zmax, true, target, 0.0, kmax, kmin, sh);
+      cp = radix_cut<BLOCK>(zat, V, zmax, true, target, 0.0, kmax, kmin, sh);
     } else {
-      cp = radix_cut<BLOCK>(z, V, zmax, true, 0ull, (double)a.top_p, kmax, kmin, sh);
+      cp = radix_cut<BLOCK>(zat, V, zmax, true, 0ull, (double)a.top_p, kmax, kmin, sh);
     }
     if (cp.cut > cut) cut = cp.cut;
   }
@@ -225,7 +221,7 @@ __device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab
   uint64_t E = 0;
   int32_t last = -1;
   for (int i = t; i < V; i += BLOCK) {
-    const float v = z[i];
+    const float v = zat(i);
     if (v == -INFINITY || composite(v, i) < cut) continue;
     const float e = rel_exp(v, zmax);
     if (use_min_p && !(e >= a.min_p)) continue;
@@ -256,7 +252,7 @@ __device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab
       w[j] = 0;
       float q = 0.0f;
       if (i < V) {
-        const float v = z[i];
+        const float v = zat(i);
         if (v != -INFINITY && composite(v, i) >= cut) {
           const float e = rel_exp(v, zmax);
           if (!use_min_p || e >= a.min_p) {

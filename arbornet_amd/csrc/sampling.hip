@@ -247,12 +247,17 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   }
   pl.lds_solver = sizeof(uint32_t) * (size_t)(1 << hb);
   size_t off = 0;
+  // Workspace per path: split streamed rows publish each chunk's list (count, flags and 64
+  // candidates); the histogram solvers keep one padded fp32 z row per row (and, split, one
+  // record per workgroup and the barrier counters). Rows streamed whole need nothing: their
+  // exact fallback recomputes z from the logits.
+  const bool chunk_lists = pl.path == Path::Stream && pl.S > 1;
   pl.off_hdr = off;
-  off = align_up(off + sizeof(uint32_t) * 2 * (size_t)B * (size_t)pl.S, 256);
+  if (chunk_lists) off = align_up(off + sizeof(uint32_t) * 2 * (size_t)B * (size_t)pl.S, 256);
   pl.off_cand = off;
-  off = align_up(off + sizeof(uint64_t) * arbor::kChunkSlot * (size_t)B * (size_t)pl.S, 256);
+  if (chunk_lists) off = align_up(off + sizeof(uint64_t) * arbor::kChunkSlot * (size_t)B * (size_t)pl.S, 256);
   pl.off_zbuf = off;
-  off = align_up(off + sizeof(float) * (size_t)B * align_up((size_t)V, 64), 256);
+  if (pl.path == Path::Solver) off = align_up(off + sizeof(float) * (size_t)B * align_up((size_t)V, 64), 256);
   pl.off_split = off;
   pl.off_ctr = off;
   if (pl.path == Path::Solver && pl.S > 1) {
@@ -260,7 +265,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.off_ctr = off;
     off = align_up(off + sizeof(uint32_t) * (2 * (size_t)B + 1), 256);  // row barriers, ticket, failure words
   }
-  pl.total = off;
+  pl.total = off > 256 ? off : 256;  // never 0: 0 reports invalid params
   return pl;
 }
 

@@ -62,7 +62,9 @@ def test_large_shape_paths(case):
     sys.stdout.flush()
     inp = syn.generate(w)
     ids, _ = run_gpu(S.params_for(w), inp, repeat=2)
-    n, nb, nbm = compare(S.params_for(w), inp, ids, label=label)
+    # top-p rows that keep tens of thousands of ids have CDF steps of ~1e-5, so a tenth to
+    # a half of them fall within 1e-6 (plus the ambiguous mass at the cut) of a step
+    n, nb, nbm = compare(S.params_for(w), inp, ids, label=label, max_boundary=max(2, (6 * B) // 10))
     print(f"[paths {case}] rows {n}, boundary {nb}, boundary rows differing {nbm}", flush=True)
     if B * V <= 80_000_000:  # probabilities of the whole batch, on the same path
         ids_p, probs = run_gpu(S.params_for(w), inp, write_probs=True)
