@@ -407,6 +407,37 @@ int launch_solver(const Plan& pl, hipStream_t st, arbor::Args a, char* ws) {
   return launch(arbor::solver_kernel<DT>, dim3((unsigned)a.B), dim3(arbor::kBlock), lds, st, a);
 }
 
+// ---------------------------------------------------------------------------------------
+// Static scratch of arbor_sample_noalloc: the workspace of callers that cannot allocate.
+// Every device the library runs on holds its own copy until the process ends. In host code
+// `scratch` names a host-side stand-in, not device memory: its device address comes from
+// hipGetSymbolAddress, once per device (with that device current), and only that address
+// is ever handed to a kernel.
+// ---------------------------------------------------------------------------------------
+constexpr size_t kScratchBytes = ARBOR_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(ARBOR_ERR_NO_DEVICE, "device %d beyond the %d this library serves", dev,
+                                                 kMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(ARBOR_ERR_NO_DEVICE, "hipGetSymbolAddress(scratch) returned NULL");
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return ARBOR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -519,6 +550,23 @@ int arbor_sample_append(const arbor_sampling_params* p, const void* logits, int3
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return ARBOR_OK;
+}
+
+int arbor_sample_noalloc(const arbor_sampling_params* p, const void* logits, const int32_t* history,
+                         const uint32_t* allow_mask, const float* uniforms, int32_t* out_ids, float* out_probs,
+                         void* stream) {
+  int st = validate(p);
+  if (st != ARBOR_OK) return st;
+  const size_t need = make_plan(p, device_cus()).total;
+  if (need > kScratchBytes)
+    return fail(ARBOR_ERR_WORKSPACE,
+                "these params need %zu bytes of workspace; the static scratch of arbor_sample_noalloc holds %zu "
+                "(call arbor_sample with a workspace of arbor_sample_workspace_bytes() instead)",
+                need, kScratchBytes);
+  void* ws = nullptr;
+  st = scratch_address(&ws);
+  if (st != ARBOR_OK) return st;
+  return arbor_sample(p, logits, history, allow_mask, uniforms, out_ids, out_probs, ws, kScratchBytes, stream);
 }
 
 int arbor_device_count(int* count) {

@@ -122,6 +122,8 @@ def library() -> ctypes.CDLL:
         lib.arbor_sample.restype = i32
         lib.arbor_sample_append.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.arbor_sample_append.restype = i32
+        lib.arbor_sample_noalloc.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
+        lib.arbor_sample_noalloc.restype = i32
         lib.arbor_sample_workspace_bytes.argtypes = [P]
         lib.arbor_sample_workspace_bytes.restype = sz
         lib.arbor_sampling_params_init.argtypes = [P, ctypes.c_int32, ctypes.c_int32]
@@ -169,6 +171,14 @@ def sample_raw(params: SamplingParams, logits: int, history: Optional[int], mask
     """Call arbor_sample with raw device addresses; returns the status (does not raise)."""
     return int(library().arbor_sample(ctypes.byref(params), logits, history, mask, uniforms, out_ids,
                                       out_probs, workspace, workspace_bytes_, stream))
+
+
+def sample_noalloc_raw(params: SamplingParams, logits: int, history: Optional[int], mask: Optional[int],
+                       uniforms: int, out_ids: int, out_probs: Optional[int], stream: Optional[int]) -> int:
+    """Call arbor_sample_noalloc (the library's static scratch is the workspace); returns
+    the status."""
+    return int(library().arbor_sample_noalloc(ctypes.byref(params), logits, history, mask, uniforms, out_ids,
+                                              out_probs, stream))
 
 
 def sample_append_raw(params: SamplingParams, logits: int, history: int, positions: int, mask: Optional[int],

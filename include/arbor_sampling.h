@@ -142,6 +142,24 @@ int arbor_sample_append(const arbor_sampling_params* params, const void* logits,
                         const float* uniforms, int32_t* out_ids, float* out_probs,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * arbor_sample without a workspace argument and without any allocation: the library's
+ * static device scratch (ARBOR_NOALLOC_SCRATCH_BYTES per device, held from the first call
+ * on a device until the process ends) serves as the workspace. Arguments and results are
+ * those of arbor_sample. Params whose arbor_sample_workspace_bytes() exceeds the scratch
+ * return ARBOR_ERR_WORKSPACE (streamed rows, top-k <= 64 or min-p alone, always fit; the
+ * histogram solver's rows fit for small batches only). Every call on one device shares
+ * that device's scratch: calls that overlap on one device race and must be ordered (one
+ * stream, or synchronised), like calls that share a workspace.
+ * No counterpart in the reference: this entry point is for callers that cannot allocate
+ * device memory, such as code under HIP graph capture, tight serving loops and harnesses
+ * that forbid hipMalloc.
+ */
+#define ARBOR_NOALLOC_SCRATCH_BYTES (16u << 20)
+int arbor_sample_noalloc(const arbor_sampling_params* params, const void* logits,
+                         const int32_t* history, const uint32_t* allow_mask,
+                         const float* uniforms, int32_t* out_ids, float* out_probs, void* stream);
+
 /* Bytes of workspace arbor_sample needs for these params (0 if params are invalid).
  * No reference counterpart: the reference's kernels need no scratch (CudaBackend.cs:43-46). */
 size_t arbor_sample_workspace_bytes(const arbor_sampling_params* params);
