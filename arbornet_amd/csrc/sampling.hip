@@ -30,6 +30,7 @@
 #include "args.hpp"
 #include "block_ops.hpp"
 #include "mass_solver.hpp"
+#include "nucleus.hpp"
 #include "row_solver.hpp"
 #include "split_solver.hpp"
 #include "topk_path.hpp"
@@ -148,7 +149,7 @@ int hip_fail(hipError_t e, const char* what) {
   return (int)e;
 }
 
-enum class Path { Stream, Solver };
+enum class Path { Stream, Nucleus, Solver };
 
 struct Plan {
   Path path;
@@ -156,7 +157,7 @@ struct Plan {
   int k;            // effective top-k (0 = off)
   int S, chunk_len;
   int hash_bits, bitmap_words;
-  size_t lds_stream, lds_solver;
+  size_t lds_stream, lds_solver, lds_nucleus;
   int mask_lds;  // byte offset of the LDS mask words (streamed masked rows), else -1
   // workspace layout (byte offsets)
   size_t off_hdr, off_cand, off_zbuf, off_split, off_ctr, total;
@@ -210,9 +211,12 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
   const int V = p->vocab, B = p->batch;
   pl.k = (p->top_k > 0 && p->top_k < V) ? p->top_k : 0;
   // the streaming top-k kernel: top-k <= 64, or min-p as the only filter (its 64-entry
-  // list then holds the min-p band); everything else goes to the row solver
+  // list then holds the min-p band); without top-k otherwise (top-p, with or without min-p,
+  // or no filter at all) the two-pass nucleus kernel; top-k above 64 the histogram solver
   const bool minp_only = pl.k == 0 && p->top_p >= 1.0f && p->min_p > 0.0f;
-  pl.path = (pl.k > 0 && pl.k <= arbor::kMaxTopK) || minp_only ? Path::Stream : Path::Solver;
+  pl.path = (pl.k > 0 && pl.k <= arbor::kMaxTopK) || minp_only ? Path::Stream
+            : pl.k == 0                                           ? Path::Nucleus
+                                                                  : Path::Solver;
   int hb = 6;
   while ((1 << hb) < 2 * p->hist_len) ++hb;
   pl.hash_bits = hb;
@@ -234,6 +238,22 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.inline_fin = S == 1;
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
     pl.lds_stream = arbor::TkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0);
+  } else if (pl.path == Path::Nucleus) {
+    // split rows over S workgroups when the batch is smaller than the chip, never below
+    // 16K ids per chunk; chunks of at most 262,144 ids (the history bitmap's reach)
+    int S = B < cus ? cus / B : 1;
+    const int by_len = (V + 16383) / 16384;
+    if (S > by_len) S = by_len;
+    if (S > arbor::kMaxChunks) S = arbor::kMaxChunks;
+    const int by_bitmap = (V + arbor::kNuMaxChunk - 1) / arbor::kNuMaxChunk;
+    if (S < by_bitmap) S = by_bitmap;
+    if (S < 1) S = 1;
+    const int len = (int)align_up((size_t)((V + S - 1) / S), 1024);
+    pl.S = (V + len - 1) / len;
+    pl.chunk_len = len;
+    const int n_batches = (len + arbor::kNuBatchIds - 1) / arbor::kNuBatchIds;
+    pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
+    pl.lds_nucleus = (size_t)arbor::NuLayout::make(n_batches, pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0).bytes;
   } else if (B < cus) {
     // row solver over S workgroups per row, never below 8K ids per chunk
     int S = cus / B;
@@ -264,6 +284,11 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     off = align_up(off + sizeof(arbor::SplitChunk) * (size_t)B * (size_t)pl.S, 256);
     pl.off_ctr = off;
     off = align_up(off + sizeof(uint32_t) * (2 * (size_t)B + 1), 256);  // row barriers, ticket, failure words
+  }
+  if (pl.path == Path::Nucleus && pl.S > 1) {
+    off = align_up(off + sizeof(arbor::NuRec) * (size_t)B * (size_t)pl.S, 256);
+    pl.off_ctr = off;
+    off = align_up(off + sizeof(uint64_t) * (2 * (size_t)B), 256);  // tagged barrier and failure words
   }
   pl.total = off > 256 ? off : 256;  // never 0: 0 reports invalid params
   return pl;
@@ -375,6 +400,47 @@ uint32_t split_spin_limit() {
     if (v > 0 && v < arbor::kSplitSpinLimit) return (uint32_t)v;
   }
   return arbor::kSplitSpinLimit;
+}
+
+// The two-pass nucleus kernel: one instance per (dtype, whole aligned units, history, mask).
+// Split rows meet at barriers whose words carry a per-call tag, taken from a counter shared
+// by every call of the process, so the workspace needs no clearing between calls.
+uint32_t next_call_tag() {
+  static std::atomic<uint32_t> tag{0};
+  uint32_t t = tag.fetch_add(1u, std::memory_order_relaxed) + 1u;
+  if (t == 0u) t = tag.fetch_add(1u, std::memory_order_relaxed) + 1u;  // 0 never tags a call
+  return t;
+}
+
+template <int DT, bool ALIGNED, bool PEN, bool MASK>
+int launch_nucleus4(const Plan& pl, hipStream_t st, const arbor::Args& a, char* ws) {
+  auto kernel = arbor::nucleus_kernel<DT, ALIGNED, PEN, MASK>;
+  if (pl.lds_nucleus > 64 * 1024) {
+    const int r = allow_lds(reinterpret_cast<const void*>(kernel), pl.lds_nucleus);
+    if (r != ARBOR_OK) return r;
+  }
+  arbor::NuRec* recs = pl.S > 1 ? reinterpret_cast<arbor::NuRec*>(ws + pl.off_split) : nullptr;
+  uint64_t* ctr = pl.S > 1 ? reinterpret_cast<uint64_t*>(ws + pl.off_ctr) : nullptr;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)(a.B * pl.S)), dim3(arbor::kNuBlock), pl.lds_nucleus, st, a, recs, ctr,
+                     next_call_tag(), split_spin_limit());
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return ARBOR_OK;
+}
+
+template <int DT, bool ALIGNED>
+int launch_nucleus2(const Plan& pl, bool pen, bool mask, hipStream_t st, const arbor::Args& a, char* ws) {
+  if (pen) return mask ? launch_nucleus4<DT, ALIGNED, true, true>(pl, st, a, ws)
+                       : launch_nucleus4<DT, ALIGNED, true, false>(pl, st, a, ws);
+  return mask ? launch_nucleus4<DT, ALIGNED, false, true>(pl, st, a, ws)
+              : launch_nucleus4<DT, ALIGNED, false, false>(pl, st, a, ws);
+}
+
+template <int DT>
+int launch_nucleus(const Plan& pl, bool pen, bool mask, hipStream_t st, const arbor::Args& a, char* ws) {
+  // whole 16-byte units only: aligned rows whose length is a multiple of the unit
+  if (a.aligned && a.V % arbor::Elem<DT>::kVec == 0) return launch_nucleus2<DT, true>(pl, pen, mask, st, a, ws);
+  return launch_nucleus2<DT, false>(pl, pen, mask, st, a, ws);
 }
 
 // The row solver: S workgroups per row when the plan splits rows and the grid can be
@@ -529,6 +595,11 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   if (pl.path == Path::Solver) {
     if (p->dtype == ARBOR_DTYPE_BF16) return launch_solver<ARBOR_DTYPE_BF16>(pl, s, a, ws);
     return launch_solver<ARBOR_DTYPE_F32>(pl, s, a, ws);
+  }
+  if (pl.path == Path::Nucleus) {
+    const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
+    if (p->dtype == ARBOR_DTYPE_BF16) return launch_nucleus<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a, ws);
+    return launch_nucleus<ARBOR_DTYPE_F32>(pl, pen, mask, s, a, ws);
   }
   const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
   if (p->dtype == ARBOR_DTYPE_BF16) return launch_topk<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a);

@@ -41,6 +41,11 @@ CASES = [
     # each row into chunks (the chunk's history bitmap holds at most 262,144 ids)
     ("top-k 50 stream at ARBOR_VOCAB_MAX, B=256 bf16", 256, 1048575, "bf16", dict(top_k=50, top_p=0.95), 2),
     ("top-k 50 stream at ARBOR_VOCAB_MAX, B=2", 2, 1048575, "f32", dict(top_k=50), 2),
+    # the two-pass top-p kernel with min-p beside top-p, on c4's inputs (min-p's edge far
+    # above top-p's cut, so min-p decides), rows split over workgroups and whole
+    ("c4 inputs, top-p 0.9 + min-p 0.05, B=64", -64, 152064, "bf16", dict(top_p=0.9), 4),
+    ("c4 inputs, top-p 0.9 + min-p 0.05, B=256", -256, 152064, "bf16", dict(top_p=0.9), 4),
+    ("c4 inputs, top-p 0.3 + min-p 0.01, B=64", -64, 152064, "bf16", dict(top_p=0.3, min_p=0.01), 4),
 ]
 
 
@@ -57,7 +62,10 @@ def _device():
 @pytest.mark.parametrize("case", range(len(CASES)), ids=lambda i: CASES[i][0])
 def test_large_shape_paths(case):
     label, B, V, dtype, kw, nprob = CASES[case]
-    w = BASE.scaled(batch=B, vocab=V, dtype=dtype, seed=40 + case, **kw)
+    base = BASE
+    if B < 0:  # c4's inputs and parameters
+        base, B = syn.CONFIGS["c4"], -B
+    w = base.scaled(batch=B, vocab=V, dtype=dtype, seed=40 + case, **kw)
     print(f"[paths {case}] {label}: B={B} V={V} {dtype} {kw}", flush=True)
     sys.stdout.flush()
     inp = syn.generate(w)

@@ -62,8 +62,9 @@ def _both(w: syn.Workload, write_probs=False):
 CASES = [
     # (label, first workload, second (smaller) workload)
     ("streamed rows in chunks (c5 shape)", syn.CONFIGS["c5"], syn.CONFIGS["c5"].scaled(batch=32, vocab=64000)),
-    ("split histogram solver (top-p only)", syn.CONFIGS["c2"].scaled(batch=8, vocab=32000, hist_len=64),
-     syn.CONFIGS["c2"].scaled(batch=4, vocab=20000, hist_len=16, seed=9)),
+    ("split histogram solver (top-k 200, top-p)", syn.CONFIGS["c2"].scaled(batch=8, vocab=32000, hist_len=64, top_k=200),
+     syn.CONFIGS["c2"].scaled(batch=4, vocab=20000, hist_len=16, seed=9, top_k=200)),
+    ("two-pass top-p kernel", syn.CONFIGS["c2"], syn.CONFIGS["c2"].scaled(batch=16, vocab=50000, seed=10)),
     ("streamed top-k, one chunk per row", syn.CONFIGS["c3"].scaled(batch=256),
      syn.CONFIGS["c3"].scaled(batch=64, vocab=50000, seed=8)),
 ]
@@ -83,8 +84,9 @@ def test_noalloc_matches_workspace_call(case):
 
 
 def test_noalloc_rejects_params_beyond_the_scratch():
-    # top-p only at B=64, V=128256 (c2) needs a z row per row: 32.8 MB > 16 MB of scratch
-    p = S.params_for(syn.CONFIGS["c2"])
+    # top-k 300 at B=64, V=128256 takes the histogram solver, which needs a z row per row
+    # (32.8 MB) and its split records: more than the 16 MB of scratch
+    p = S.params_for(syn.CONFIGS["c2"].scaled(top_k=300))
     assert S.workspace_bytes(p) > SCRATCH
     st = S.sample_noalloc_raw(p, 16, 16, None, 16, 16, None, None)
     assert st == -12
