@@ -33,6 +33,7 @@
 #include "nucleus.hpp"
 #include "row_solver.hpp"
 #include "split_solver.hpp"
+#include "tokens.hpp"
 #include "topk_path.hpp"
 #include "topk_stream.hpp"
 
@@ -638,6 +639,43 @@ int arbor_sample_noalloc(const arbor_sampling_params* p, const void* logits, con
   st = scratch_address(&ws);
   if (st != ARBOR_OK) return st;
   return arbor_sample(p, logits, history, allow_mask, uniforms, out_ids, out_probs, ws, kScratchBytes, stream);
+}
+
+int arbor_decode(const int32_t* ids, int32_t count, const int32_t* token_offsets, const uint8_t* token_bytes,
+                 int32_t vocab, int32_t unk_id, int32_t* out_offsets, uint8_t* out_bytes, size_t out_capacity,
+                 void* stream) {
+  if (count < 0 || vocab < 0) return fail(ARBOR_ERR_SHAPE, "count %d and vocab %d must be >= 0", count, vocab);
+  if (!out_offsets || (count > 0 && !ids) || (vocab > 0 && (!token_offsets || !token_bytes)) ||
+      (out_capacity > 0 && !out_bytes))
+    return fail(ARBOR_ERR_NULL, "ids, token_offsets, token_bytes, out_offsets and out_bytes are required");
+  hipLaunchKernelGGL(arbor::decode_kernel, dim3(1), dim3(arbor::kDecodeBlock), 0, static_cast<hipStream_t>(stream),
+                     ids, (int)count, token_offsets, token_bytes, (int)vocab, (int)unk_id, out_offsets, out_bytes,
+                     out_capacity);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ARBOR_OK : hip_fail(e, "kernel launch");
+}
+
+int arbor_embed(const int32_t* ids, int32_t count, const void* table, int32_t vocab, int32_t width, int32_t dtype,
+                void* out_rows, void* stream) {
+  if (count < 0 || vocab <= 0 || width <= 0)
+    return fail(ARBOR_ERR_SHAPE, "count %d >= 0, vocab %d > 0 and width %d > 0 are required", count, vocab, width);
+  if (dtype != ARBOR_DTYPE_F32 && dtype != ARBOR_DTYPE_BF16) return fail(ARBOR_ERR_DTYPE, "unknown dtype %d", dtype);
+  if (count == 0) return ARBOR_OK;
+  if (!ids || !table || !out_rows) return fail(ARBOR_ERR_NULL, "ids, table and out_rows are required");
+  const size_t row_bytes = (size_t)width * (dtype == ARBOR_DTYPE_BF16 ? 2 : 4);
+  if (row_bytes > (size_t)INT32_MAX) return fail(ARBOR_ERR_SHAPE, "rows of %zu bytes are too long", row_bytes);
+  const bool units = row_bytes % 16 == 0 && (uintptr_t)table % 16 == 0 && (uintptr_t)out_rows % 16 == 0;
+  const unsigned nx = (unsigned)((row_bytes / (units ? 16 : 1) + 255) / 256);
+  const dim3 grid(units ? nx : (nx < 64u ? nx : 64u), (unsigned)count);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned char* tb = static_cast<const unsigned char*>(table);
+  unsigned char* ob = static_cast<unsigned char*>(out_rows);
+  if (units)
+    hipLaunchKernelGGL(arbor::embed_kernel<true>, grid, dim3(256), 0, s, ids, tb, (int)vocab, (int)row_bytes, ob);
+  else
+    hipLaunchKernelGGL(arbor::embed_kernel<false>, grid, dim3(256), 0, s, ids, tb, (int)vocab, (int)row_bytes, ob);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ARBOR_OK : hip_fail(e, "kernel launch");
 }
 
 int arbor_device_count(int* count) {

@@ -122,6 +122,10 @@ def library() -> ctypes.CDLL:
         lib.arbor_sample.restype = i32
         lib.arbor_sample_append.argtypes = [P, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
         lib.arbor_sample_append.restype = i32
+        lib.arbor_decode.argtypes = [vp, ctypes.c_int32, vp, vp, ctypes.c_int32, ctypes.c_int32, vp, vp, sz, vp]
+        lib.arbor_decode.restype = i32
+        lib.arbor_embed.argtypes = [vp, ctypes.c_int32, vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, vp, vp]
+        lib.arbor_embed.restype = i32
         lib.arbor_sample_noalloc.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
         lib.arbor_sample_noalloc.restype = i32
         lib.arbor_sample_workspace_bytes.argtypes = [P]
@@ -341,3 +345,72 @@ class GenerationState:
         check(sample_append_raw(p, logits.data_ptr(), self.history.data_ptr(), self.positions.data_ptr(), mask_ptr,
                                 uniforms.data_ptr(), out_ids.data_ptr(), None, ws.data_ptr(), ws.numel(), stream))
         return out_ids
+
+
+class TokenTable:
+    """A tokenizer vocabulary on the device as an id -> bytes table (CSR), for decoding
+    sampled ids in one launch (arbor_decode). Mirrors the reference's Decode
+    (ArborNet.Data/Tokenizers.cs:191-200, :304-313): the text of id t is the first key of the
+    vocabulary (in its order) that maps to t, the unknown token when none does or t lies
+    outside the vocabulary; the texts are joined with nothing between them."""
+
+    def __init__(self, vocab: dict, unk_token: str, device="cuda"):
+        import numpy as np
+        import torch
+
+        n = max(vocab.values(), default=-1) + 1
+        text = [None] * n
+        for key, v in vocab.items():
+            if 0 <= v < n and text[v] is None:
+                text[v] = key
+        self.vocab = n
+        self.unk_id = vocab.get(unk_token, -1)
+        blobs = [(t if t is not None else unk_token).encode("utf-8") for t in text]
+        offsets = np.zeros(n + 1, dtype=np.int32)
+        offsets[1:] = np.cumsum([len(b) for b in blobs], dtype=np.int64)
+        data = np.frombuffer(b"".join(blobs) or b"\0", dtype=np.uint8).copy()
+        self.offsets = torch.from_numpy(offsets).to(device)
+        self.bytes = torch.from_numpy(data).to(device)
+        self.device = torch.device(device)
+
+    def decode_raw(self, ids, capacity: Optional[int] = None):
+        """(out_offsets [count + 1], out_bytes) of device ids (int32 tensor), on the current
+        stream; raises ArborSamplingError on a nonzero status."""
+        import torch
+
+        ids = ids.to(device=self.device, dtype=torch.int32).contiguous()
+        count = ids.numel()
+        cap = 64 * max(count, 1) if capacity is None else capacity
+        offs = torch.empty(count + 1, dtype=torch.int32, device=self.device)
+        out = torch.empty(max(cap, 1), dtype=torch.uint8, device=self.device)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        check(int(library().arbor_decode(ids.data_ptr(), count, self.offsets.data_ptr(), self.bytes.data_ptr(),
+                                         self.vocab, self.unk_id, offs.data_ptr(), out.data_ptr(), cap, stream)))
+        return offs, out
+
+    def decode(self, ids) -> str:
+        """The text of a batch of ids (one launch; a second one if the first ran out of room)."""
+        offs, out = self.decode_raw(ids)
+        total = int(offs[-1].item())
+        if total > out.numel():
+            offs, out = self.decode_raw(ids, capacity=total)
+        return bytes(out[:total].cpu().numpy()).decode("utf-8", errors="replace")
+
+
+def embed(ids, table, out=None):
+    """out[i, :] = table[ids[i], :] on the device (zeros for ids outside the table), the
+    embedding gather a generation loop feeds its next forward pass (arbor_embed)."""
+    import torch
+
+    if table.dim() != 2 or not table.is_contiguous():
+        raise ValueError("table must be a contiguous [vocab, width] tensor")
+    dtype = {torch.float32: ARBOR_DTYPE_F32, torch.bfloat16: ARBOR_DTYPE_BF16}.get(table.dtype)
+    if dtype is None:
+        raise ArborSamplingError(-4, f"table dtype {table.dtype} is not float32 or bfloat16")
+    ids = ids.to(device=table.device, dtype=torch.int32).contiguous()
+    if out is None:
+        out = torch.empty((ids.numel(), table.shape[1]), dtype=table.dtype, device=table.device)
+    stream = torch.cuda.current_stream(table.device).cuda_stream
+    check(int(library().arbor_embed(ids.data_ptr(), ids.numel(), table.data_ptr(), table.shape[0], table.shape[1],
+                                    dtype, out.data_ptr(), stream)))
+    return out

@@ -160,6 +160,34 @@ int arbor_sample_noalloc(const arbor_sampling_params* params, const void* logits
                          const int32_t* history, const uint32_t* allow_mask,
                          const float* uniforms, int32_t* out_ids, float* out_probs, void* stream);
 
+/*
+ * Text of sampled ids: a tokenizer vocabulary held on the device as an id -> bytes table
+ * (token_offsets [vocab + 1] int32, ascending; token_bytes the UTF-8 bytes of every token,
+ * token t being bytes [token_offsets[t], token_offsets[t + 1])). Ids outside [0, vocab)
+ * decode as token unk_id (nothing if unk_id is outside it too).
+ *   ids           [count] int32 (device), e.g. the out_ids of arbor_sample
+ *   out_offsets   [count + 1] int32 (device): where each id's text starts in out_bytes;
+ *                 out_offsets[count] = total bytes (must stay below 2^31)
+ *   out_bytes     device buffer of out_capacity bytes; bytes past the capacity are not
+ *                 written (out_offsets[count] still reports what the text needs)
+ * Replaces the per-token vocabulary scan of the reference's Decode
+ * (ArborNet.Data/Tokenizers.cs:191-200 BPE, :304-313 SentencePiece: FirstOrDefault over the
+ * vocabulary for each id, the unknown token when none matches): one launch for a batch.
+ */
+int arbor_decode(const int32_t* ids, int32_t count, const int32_t* token_offsets, const uint8_t* token_bytes,
+                 int32_t vocab, int32_t unk_id, int32_t* out_offsets, uint8_t* out_bytes, size_t out_capacity,
+                 void* stream);
+
+/*
+ * The embedding rows of ids, for the next forward pass of a generation loop:
+ * out_rows[i, :] = table[ids[i], :], a zero row for ids outside [0, vocab) (sentinels).
+ *   table     [vocab, width] fp32 or bf16 (dtype, device); out_rows [count, width], same dtype
+ * Replaces ArborNet.Layers/Embedding.cs:53-57, whose Forward returns the whole weight table
+ * instead of gathering the rows of its indices.
+ */
+int arbor_embed(const int32_t* ids, int32_t count, const void* table, int32_t vocab, int32_t width, int32_t dtype,
+                void* out_rows, void* stream);
+
 /* Bytes of workspace arbor_sample needs for these params (0 if params are invalid).
  * No reference counterpart: the reference's kernels need no scratch (CudaBackend.cs:43-46). */
 size_t arbor_sample_workspace_bytes(const arbor_sampling_params* params);
