@@ -45,6 +45,10 @@ struct Args {
   uint64_t* cand;  // [B*S*kChunkSlot]   sorted candidate composites of each chunk
   float* zbuf;     // [B*ldz]            row solver's tempered logits
   int ldz;         // zbuf row stride: V rounded up to 64 floats (rows 256-byte aligned)
+  // generation step (streamed rows only): the history ring and its write positions; the
+  // thread that writes a row's id also appends it, after the row's history was read
+  int32_t* ring_hist;  // == hist, writable; null: no append
+  int32_t* ring_pos;   // [B]
 };
 
 template <int DT>
@@ -132,6 +136,16 @@ __device__ __forceinline__ float unpack_unit(const uint32_t* w, int j) {
 template <int DT>
 __device__ __forceinline__ const void* row_ptr(const Args& a, int row) {
   return static_cast<const char*>(a.logits) + (size_t)row * (size_t)a.ld * (size_t)Elem<DT>::kBytes;
+}
+
+// The row's sampled id goes to slot positions[row] mod H of its history ring, and the
+// position advances (sentinels append nothing). Penalties count occurrences, so the
+// ring's order does not matter. Called by the one thread that writes out_ids[row].
+__device__ __forceinline__ void ring_append(const Args& a, int row, int32_t id) {
+  if (a.ring_pos == nullptr || id < 0) return;
+  const uint32_t pos = (uint32_t)a.ring_pos[row];
+  a.ring_hist[(size_t)row * (size_t)a.H + pos % (uint32_t)a.H] = id;
+  a.ring_pos[row] = (int32_t)(pos + 1u);
 }
 
 }  // namespace arbor

@@ -282,7 +282,11 @@ __device__ __forceinline__ void solve_row(const Args& a, int row, uint32_t* htab
     __syncthreads();
     if (sh.b32[2] >= 0 && !prow) break;
   }
-  if (t == 0) a.out_ids[row] = sh.b32[2] >= 0 ? sh.b32[2] : last;
+  if (t == 0) {
+    const int32_t pick = sh.b32[2] >= 0 ? sh.b32[2] : last;
+    a.out_ids[row] = pick;
+    ring_append(a, row, pick);  // the row's history was read in step 1, before the barriers
+  }
 }
 
 }  // namespace arbor

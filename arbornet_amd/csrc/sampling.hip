@@ -532,9 +532,13 @@ size_t arbor_sample_workspace_bytes(const arbor_sampling_params* p) {
   return make_plan(p, device_cus()).total;
 }
 
-int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32_t* history,
-                 const uint32_t* allow_mask, const float* uniforms, int32_t* out_ids, float* out_probs,
-                 void* workspace, size_t workspace_bytes, void* stream) {
+// arbor_sample's body. With ring_pos set (a generation step), streamed rows append their id
+// to the history ring in the kernel that draws it, and *appended says so; the other paths
+// leave the append to the caller.
+static int sample_impl(const arbor_sampling_params* p, const void* logits, const int32_t* history,
+                       const uint32_t* allow_mask, const float* uniforms, int32_t* out_ids, float* out_probs,
+                       void* workspace, size_t workspace_bytes, void* stream, int32_t* ring_hist, int32_t* ring_pos,
+                       bool* appended) {
   int st = validate(p);
   if (st != ARBOR_OK) return st;
   if (!logits || !uniforms || !out_ids) return fail(ARBOR_ERR_NULL, "logits, uniforms and out_ids are required");
@@ -591,6 +595,11 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   a.cand = reinterpret_cast<uint64_t*>(ws + pl.off_cand);
   a.zbuf = reinterpret_cast<float*>(ws + pl.off_zbuf);
   a.ldz = (int)align_up((size_t)p->vocab, 64);
+  if (ring_pos && pl.path == Path::Stream) {
+    a.ring_hist = ring_hist;
+    a.ring_pos = ring_pos;
+    *appended = true;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (pl.path == Path::Solver) {
@@ -607,6 +616,13 @@ int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32
   return launch_topk<ARBOR_DTYPE_F32>(pl, pen, mask, s, a);
 }
 
+int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32_t* history,
+                 const uint32_t* allow_mask, const float* uniforms, int32_t* out_ids, float* out_probs,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  return sample_impl(p, logits, history, allow_mask, uniforms, out_ids, out_probs, workspace, workspace_bytes, stream,
+                     nullptr, nullptr, nullptr);
+}
+
 int arbor_sample_append(const arbor_sampling_params* p, const void* logits, int32_t* history, int32_t* positions,
                         const uint32_t* allow_mask, const float* uniforms, int32_t* out_ids, float* out_probs,
                         void* workspace, size_t workspace_bytes, void* stream) {
@@ -614,8 +630,10 @@ int arbor_sample_append(const arbor_sampling_params* p, const void* logits, int3
   if (st != ARBOR_OK) return st;
   if (p->hist_len <= 0 || !history || !positions)
     return fail(ARBOR_ERR_HISTORY, "a history ring (hist_len > 0) and positions are required");
-  st = arbor_sample(p, logits, history, allow_mask, uniforms, out_ids, out_probs, workspace, workspace_bytes, stream);
-  if (st != ARBOR_OK) return st;
+  bool appended = false;
+  st = sample_impl(p, logits, history, allow_mask, uniforms, out_ids, out_probs, workspace, workspace_bytes, stream,
+                   history, positions, &appended);
+  if (st != ARBOR_OK || appended) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(arbor::append_kernel, dim3((unsigned)((p->batch + 255) / 256)), dim3(256), 0, s, history,
                      (int)p->hist_len, positions, out_ids, (int)p->batch);

@@ -118,7 +118,10 @@ __device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t bes
   const uint64_t over = __ballot(kk && cid > target);
   const int pick = over ? 63 - __builtin_clzll(over) : __ffsll((long long)__ballot(kk)) - 1;
   const int32_t pick_id = (int32_t)((lane_get(key, pick) >> 6) & 0xFFFFFu);
-  if (lane == 0) a.out_ids[row] = pick_id;
+  if (lane == 0) {
+    a.out_ids[row] = pick_id;
+    ring_append(a, row, pick_id);
+  }
   if (a.write_probs && kk) a.out_probs[(size_t)row * (size_t)a.V + ((key >> 6) & 0xFFFFFu)] = (float)(er / E);
 }
 __device__ __forceinline__ void finish_list(const Args& a, int row, uint64_t best, int n) {

@@ -133,6 +133,9 @@ int arbor_sample(const arbor_sampling_params* params, const void* logits,
  *               goes to slot positions[b] mod hist_len and positions[b] advances. Rows
  *               whose result is a sentinel (ARBOR_ID_*) append nothing.
  *   the other arguments as for arbor_sample.
+ * Streamed rows (top-k <= 64, or min-p alone) are appended by the kernel that draws them,
+ * so such a step is one launch; the other paths append in a second, one-thread-per-row
+ * launch.
  * No counterpart in the reference: its models return [batch, seq, vocab] logits
  * (ArborNet.Models/GPT.cs:96-111, Llama3.cs:67-74) and nothing consumes them; this is the
  * step a generation loop around those Forward calls would make.

@@ -43,6 +43,12 @@ LOOPS = [
                                        presence_penalty=0.2, top_k=20, top_p=0.9)),
     (6, 20000, 1, 64, 30, "bf16", dict(temperature=1.2, repetition_penalty=1.5, min_p=0.05)),
     (4, 40000, 2, 8, 25, "f32", dict(repetition_penalty=0.8, top_p=0.7)),  # split row solver, raising penalty
+    # a batch that fills the chip: one workgroup per row, the id appended by the kernel that draws it
+    (256, 32000, 1, 32, 4, "f32", dict(temperature=0.7, repetition_penalty=1.15, top_k=50, top_p=0.95)),
+    # near-flat rows: the min-p band overflows the 64-entry list and the same workgroup
+    # solves each row exactly, appending from the radix solver
+    (256, 4096, 1, 16, 3, "bf16", dict(min_p=0.05, repetition_penalty=1.1, _scale=0.01)),
+    (300, 6000, 1, 16, 3, "f32", dict(top_k=100, _scale=0.5)),  # k > 64: the histogram solver, then an append launch
 ]
 
 
@@ -51,15 +57,17 @@ def test_generation_loop_matches_oracle(case):
     import torch
 
     B, V, seq, H, steps, dtype, kw = LOOPS[case]
+    kw = dict(kw)
+    scale = kw.pop("_scale", 2.0)
     print(f"[generation {case}] B={B} V={V} seq={seq} H={H} steps={steps} {dtype} {kw}", flush=True)
     rng = np.random.default_rng(50 + case)
-    base = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    base = (rng.standard_normal((B, V)) * scale).astype(np.float32)
     state = S.GenerationState(B, H, "cuda:0", prompt=rng.integers(0, V, size=(B, 5), dtype=np.int32))
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     for step in range(steps):
         # the model's [B, seq, V] output; its last position changes a little every step
         x = np.repeat(base[:, None, :], seq, axis=1)
-        x[:, -1, :] += (rng.standard_normal((B, V)) * 0.5).astype(np.float32)
+        x[:, -1, :] += (rng.standard_normal((B, V)) * (scale / 4)).astype(np.float32)
         logits = torch.from_numpy(x).to("cuda:0", dtype=tdt)
         u = rng.random(B).astype(np.float32)
         hist_before = state.history.cpu().numpy()
