@@ -36,6 +36,7 @@ struct Args {
   float top_p;        // 1 = off
   float min_p;        // 0 = off
   float ln_min_p_lo;  // ln(min_p) minus a safety margin: the min-p candidate band
+  double ln_min_p;    // ln(min_p) in fp64: z is in the band iff (double)z - zmax >= ln_min_p
   int S, chunk_len;
   int hash_bits, bitmap_words;
   int mask_lds;  // masked streamed rows: byte offset of the chunk's allow-mask words in dynamic LDS
@@ -45,8 +46,9 @@ struct Args {
   uint64_t* cand;  // [B*S*kChunkSlot]   sorted candidate composites of each chunk
   float* zbuf;     // [B*ldz]            row solver's tempered logits
   int ldz;         // zbuf row stride: V rounded up to 64 floats (rows 256-byte aligned)
-  // generation step (streamed rows only): the history ring and its write positions; the
-  // thread that writes a row's id also appends it, after the row's history was read
+  // generation step (rows finished by one workgroup): the history ring and its write
+  // positions; the thread that writes a row's id also appends it, after the row's history
+  // was read
   int32_t* ring_hist;  // == hist, writable; null: no append
   int32_t* ring_pos;   // [B]
 };

@@ -960,14 +960,22 @@ __global__ void __launch_bounds__(kNuBlock) nucleus_kernel(Args a, NuRec* recs, 
     }
     __syncthreads();
     if (t == 0) {
-      if (S > 1) store_row_id(a.out_ids + row, s.pick);
-      else a.out_ids[row] = s.pick;
+      if (S > 1) {
+        store_row_id(a.out_ids + row, s.pick);
+      } else {
+        a.out_ids[row] = s.pick;
+        ring_append(a, row, s.pick);  // one workgroup: the row's history was read at the start
+      }
     }
   } else if (!(target < kept_mass) && lastk >= c0 && lastk < c1) {
     // no crossing (u * E rounds to E, or u is NaN): the last kept id, by its chunk
     if (t == 0) {
-      if (S > 1) store_row_id(a.out_ids + row, lastk);
-      else a.out_ids[row] = lastk;
+      if (S > 1) {
+        store_row_id(a.out_ids + row, lastk);
+      } else {
+        a.out_ids[row] = lastk;
+        ring_append(a, row, lastk);
+      }
     }
   }
   if (prow) {

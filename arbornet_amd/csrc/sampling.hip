@@ -66,8 +66,20 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
   }
   __syncthreads();
   const uint32_t flags = s_flags;
+  // min-p band rows (top_k 0) go to the band solver, from the merged list's top (a chunk
+  // that overflowed published nothing, so the solver checks that top against the row)
+  __shared__ uint32_t s_top;
+  const bool band = a.top_k == 0;
+  uint32_t* htab = reinterpret_cast<uint32_t*>(smem);
+  unsigned char* band_lds = smem + (sizeof(uint32_t) << a.hash_bits);
+  const bool whole = a.aligned && a.V % Elem<DT>::kVec == 0;
   if ((flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid))) {
-    solve_row<kBlock, DT>(a, row, reinterpret_cast<uint32_t*>(smem), ssh);
+    if (band && whole)
+      solve_band_row<kBlock, DT, true>(a, row, 0u, htab, band_lds);
+    else if (band)
+      solve_band_row<kBlock, DT, false>(a, row, 0u, htab, band_lds);
+    else
+      solve_row<kBlock, DT>(a, row, htab, ssh);
     return;
   }
   // wave 0 merges the chunks' lists; with min-p as the only filter (top_k 0) the merged
@@ -92,13 +104,18 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
         if (cb + j < a.S) best = list_merge(best, v[j]);
     }
     const uint64_t last = lane_get(best, kWave - 1), top = lane_get(best, 0);
-    if (lane == 0)
-      s_exact = a.top_k == 0 && last != 0ull && composite_z(last) >= composite_z(top) + a.ln_min_p_lo &&
+    if (lane == 0) {
+      s_exact = band && last != 0ull && composite_z(last) >= composite_z(top) + a.ln_min_p_lo &&
                 !(flags & (kFlagBadHistory | kFlagInvalid));
+      s_top = (uint32_t)(top >> 32);
+    }
   }
   __syncthreads();
   if (s_exact) {
-    solve_row<kBlock, DT>(a, row, reinterpret_cast<uint32_t*>(smem), ssh);
+    if (whole)
+      solve_band_row<kBlock, DT, true>(a, row, s_top, htab, band_lds);
+    else
+      solve_band_row<kBlock, DT, false>(a, row, s_top, htab, band_lds);
     return;
   }
   if (threadIdx.x >= kWave) return;
@@ -114,9 +131,10 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
   }
 }
 
-// One generation step's history update: each row's sampled id (sentinels excluded) goes
-// to slot positions[b] mod H of the row's ring, and positions[b] advances. Penalties
-// count occurrences, so the ring's order does not matter.
+// One generation step's history update, for the paths whose kernels do not append
+// themselves: each row's sampled id (sentinels excluded) goes to slot positions[b] mod H of
+// the row's ring, and positions[b] advances. Penalties count occurrences, so the ring's
+// order does not matter.
 __global__ void append_kernel(int32_t* history, int H, int32_t* positions, const int32_t* ids, int B) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
@@ -160,6 +178,7 @@ struct Plan {
   int hash_bits, bitmap_words;
   size_t lds_stream, lds_solver, lds_nucleus;
   int mask_lds;  // byte offset of the LDS mask words (streamed masked rows), else -1
+  size_t lds_finish;  // topk_finish_kernel: history table (+ the band solver's scratch)
   // workspace layout (byte offsets)
   size_t off_hdr, off_cand, off_zbuf, off_split, off_ctr, total;
 };
@@ -207,6 +226,26 @@ int device_cus() {
   return n;
 }
 
+// The nucleus kernel's split: S workgroups per row when the batch is smaller than the chip,
+// never below 16K ids per chunk; chunks of at most 262,144 ids (the history bitmap's reach).
+void nucleus_geometry(const arbor_sampling_params* p, int cus, int hash_bits, int* S_out, int* len_out,
+                      int* bitmap_words, size_t* lds) {
+  const int V = p->vocab, B = p->batch;
+  int S = B < cus ? cus / B : 1;
+  const int by_len = (V + 16383) / 16384;
+  if (S > by_len) S = by_len;
+  if (S > arbor::kMaxChunks) S = arbor::kMaxChunks;
+  const int by_bitmap = (V + arbor::kNuMaxChunk - 1) / arbor::kNuMaxChunk;
+  if (S < by_bitmap) S = by_bitmap;
+  if (S < 1) S = 1;
+  const int len = (int)align_up((size_t)((V + S - 1) / S), 1024);
+  *S_out = (V + len - 1) / len;
+  *len_out = len;
+  const int n_batches = (len + arbor::kNuBatchIds - 1) / arbor::kNuBatchIds;
+  *bitmap_words = p->hist_len > 0 ? len / 32 : 0;
+  *lds = (size_t)arbor::NuLayout::make(n_batches, *bitmap_words, p->hist_len > 0 ? (1 << hash_bits) : 0).bytes;
+}
+
 Plan make_plan(const arbor_sampling_params* p, int cus) {
   Plan pl{};
   const int V = p->vocab, B = p->batch;
@@ -240,21 +279,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
     pl.lds_stream = arbor::TkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0);
   } else if (pl.path == Path::Nucleus) {
-    // split rows over S workgroups when the batch is smaller than the chip, never below
-    // 16K ids per chunk; chunks of at most 262,144 ids (the history bitmap's reach)
-    int S = B < cus ? cus / B : 1;
-    const int by_len = (V + 16383) / 16384;
-    if (S > by_len) S = by_len;
-    if (S > arbor::kMaxChunks) S = arbor::kMaxChunks;
-    const int by_bitmap = (V + arbor::kNuMaxChunk - 1) / arbor::kNuMaxChunk;
-    if (S < by_bitmap) S = by_bitmap;
-    if (S < 1) S = 1;
-    const int len = (int)align_up((size_t)((V + S - 1) / S), 1024);
-    pl.S = (V + len - 1) / len;
-    pl.chunk_len = len;
-    const int n_batches = (len + arbor::kNuBatchIds - 1) / arbor::kNuBatchIds;
-    pl.bitmap_words = p->hist_len > 0 ? len / 32 : 0;
-    pl.lds_nucleus = (size_t)arbor::NuLayout::make(n_batches, pl.bitmap_words, p->hist_len > 0 ? (1 << hb) : 0).bytes;
+    nucleus_geometry(p, cus, hb, &pl.S, &pl.chunk_len, &pl.bitmap_words, &pl.lds_nucleus);
   } else if (B < cus) {
     // row solver over S workgroups per row, never below 8K ids per chunk
     int S = cus / B;
@@ -267,6 +292,7 @@ Plan make_plan(const arbor_sampling_params* p, int cus) {
     }
   }
   pl.lds_solver = sizeof(uint32_t) * (size_t)(1 << hb);
+  pl.lds_finish = pl.lds_solver + (pl.path == Path::Stream && pl.k == 0 ? arbor::band_lds_bytes(V, arbor::kBlock) : 0);
   size_t off = 0;
   // Workspace per path: split streamed rows publish each chunk's list (count, flags and 64
   // candidates); the histogram solvers keep one padded fp32 z row per row (and, split, one
@@ -341,7 +367,7 @@ int launch_topk5(const Plan& pl, hipStream_t st, const arbor::Args& a) {
               ? launch(arbor::topk_kernel<DT, PEN, MASK, true, ALIGNED, BAND>, grid, block, pl.lds_stream, st, a)
               : launch(arbor::topk_kernel<DT, PEN, MASK, false, ALIGNED, BAND>, grid, block, pl.lds_stream, st, a);
   if (r != ARBOR_OK || pl.inline_fin) return r;
-  return launch(arbor::topk_finish_kernel<DT>, dim3((unsigned)a.B), dim3(arbor::kBlock), pl.lds_solver, st, a);
+  return launch(arbor::topk_finish_kernel<DT>, dim3((unsigned)a.B), dim3(arbor::kBlock), pl.lds_finish, st, a);
 }
 
 // min-p as the only filter (top_k 0) compiles the band rules in
@@ -532,13 +558,24 @@ size_t arbor_sample_workspace_bytes(const arbor_sampling_params* p) {
   return make_plan(p, device_cus()).total;
 }
 
-// arbor_sample's body. With ring_pos set (a generation step), streamed rows append their id
-// to the history ring in the kernel that draws it, and *appended says so; the other paths
-// leave the append to the caller.
+// Appends every row's sampled id to its history ring, for kernels that do not append
+// themselves.
+static int launch_append(const arbor_sampling_params* p, hipStream_t s, int32_t* ring_hist, int32_t* ring_pos,
+                         const int32_t* out_ids) {
+  hipLaunchKernelGGL(arbor::append_kernel, dim3((unsigned)((p->batch + 255) / 256)), dim3(256), 0, s, ring_hist,
+                     (int)p->hist_len, ring_pos, out_ids, (int)p->batch);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return ARBOR_OK;
+}
+
+// arbor_sample's body; with ring_pos set (a generation step) it also appends each row's id
+// to the row's history ring. Kernels that finish a row in one workgroup append it
+// themselves, after the row's history was read; rows finished by split workgroups (which
+// may still end ARBOR_ID_STALLED after another chunk drew) are appended by a second launch.
 static int sample_impl(const arbor_sampling_params* p, const void* logits, const int32_t* history,
                        const uint32_t* allow_mask, const float* uniforms, int32_t* out_ids, float* out_probs,
-                       void* workspace, size_t workspace_bytes, void* stream, int32_t* ring_hist, int32_t* ring_pos,
-                       bool* appended) {
+                       void* workspace, size_t workspace_bytes, void* stream, int32_t* ring_hist, int32_t* ring_pos) {
   int st = validate(p);
   if (st != ARBOR_OK) return st;
   if (!logits || !uniforms || !out_ids) return fail(ARBOR_ERR_NULL, "logits, uniforms and out_ids are required");
@@ -581,6 +618,7 @@ static int sample_impl(const arbor_sampling_params* p, const void* logits, const
   a.top_p = p->top_p;
   a.min_p = p->min_p;
   a.ln_min_p_lo = p->min_p > 0.0f ? (float)(log((double)p->min_p) - 1e-3) : -INFINITY;
+  a.ln_min_p = p->min_p > 0.0f ? log((double)p->min_p) : -INFINITY;
   a.S = pl.S;
   a.chunk_len = pl.chunk_len;
   a.hash_bits = pl.hash_bits;
@@ -595,32 +633,39 @@ static int sample_impl(const arbor_sampling_params* p, const void* logits, const
   a.cand = reinterpret_cast<uint64_t*>(ws + pl.off_cand);
   a.zbuf = reinterpret_cast<float*>(ws + pl.off_zbuf);
   a.ldz = (int)align_up((size_t)p->vocab, 64);
-  if (ring_pos && pl.path == Path::Stream) {
-    a.ring_hist = ring_hist;
-    a.ring_pos = ring_pos;
-    *appended = true;
-  }
+  const bool bf16 = p->dtype == ARBOR_DTYPE_BF16;
+  const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (pl.path == Path::Solver) {
-    if (p->dtype == ARBOR_DTYPE_BF16) return launch_solver<ARBOR_DTYPE_BF16>(pl, s, a, ws);
-    return launch_solver<ARBOR_DTYPE_F32>(pl, s, a, ws);
+    st = bf16 ? launch_solver<ARBOR_DTYPE_BF16>(pl, s, a, ws) : launch_solver<ARBOR_DTYPE_F32>(pl, s, a, ws);
+    if (st != ARBOR_OK || !ring_pos) return st;
+    return launch_append(p, s, ring_hist, ring_pos, out_ids);
   }
   if (pl.path == Path::Nucleus) {
-    const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
-    if (p->dtype == ARBOR_DTYPE_BF16) return launch_nucleus<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a, ws);
-    return launch_nucleus<ARBOR_DTYPE_F32>(pl, pen, mask, s, a, ws);
+    if (ring_pos && pl.S == 1) {
+      a.ring_hist = ring_hist;
+      a.ring_pos = ring_pos;
+    }
+    st = bf16 ? launch_nucleus<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a, ws)
+              : launch_nucleus<ARBOR_DTYPE_F32>(pl, pen, mask, s, a, ws);
+    if (st != ARBOR_OK || !ring_pos || pl.S == 1) return st;
+    return launch_append(p, s, ring_hist, ring_pos, out_ids);
   }
-  const bool pen = p->hist_len > 0, mask = allow_mask != nullptr;
-  if (p->dtype == ARBOR_DTYPE_BF16) return launch_topk<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a);
-  return launch_topk<ARBOR_DTYPE_F32>(pl, pen, mask, s, a);
+  // streamed rows: every row is finished by one workgroup (the streaming kernel's, or the
+  // finishing kernel's for split rows), which appends it
+  if (ring_pos) {
+    a.ring_hist = ring_hist;
+    a.ring_pos = ring_pos;
+  }
+  return bf16 ? launch_topk<ARBOR_DTYPE_BF16>(pl, pen, mask, s, a) : launch_topk<ARBOR_DTYPE_F32>(pl, pen, mask, s, a);
 }
 
 int arbor_sample(const arbor_sampling_params* p, const void* logits, const int32_t* history,
                  const uint32_t* allow_mask, const float* uniforms, int32_t* out_ids, float* out_probs,
                  void* workspace, size_t workspace_bytes, void* stream) {
   return sample_impl(p, logits, history, allow_mask, uniforms, out_ids, out_probs, workspace, workspace_bytes, stream,
-                     nullptr, nullptr, nullptr);
+                     nullptr, nullptr);
 }
 
 int arbor_sample_append(const arbor_sampling_params* p, const void* logits, int32_t* history, int32_t* positions,
@@ -630,16 +675,8 @@ int arbor_sample_append(const arbor_sampling_params* p, const void* logits, int3
   if (st != ARBOR_OK) return st;
   if (p->hist_len <= 0 || !history || !positions)
     return fail(ARBOR_ERR_HISTORY, "a history ring (hist_len > 0) and positions are required");
-  bool appended = false;
-  st = sample_impl(p, logits, history, allow_mask, uniforms, out_ids, out_probs, workspace, workspace_bytes, stream,
-                   history, positions, &appended);
-  if (st != ARBOR_OK || appended) return st;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(arbor::append_kernel, dim3((unsigned)((p->batch + 255) / 256)), dim3(256), 0, s, history,
-                     (int)p->hist_len, positions, out_ids, (int)p->batch);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "kernel launch");
-  return ARBOR_OK;
+  return sample_impl(p, logits, history, allow_mask, uniforms, out_ids, out_probs, workspace, workspace_bytes, stream,
+                     history, positions);
 }
 
 int arbor_sample_noalloc(const arbor_sampling_params* p, const void* logits, const int32_t* history,

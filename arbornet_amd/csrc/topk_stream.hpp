@@ -20,7 +20,8 @@
 //     largest of them bounds the row's k-th best from below. Thresholds taken from raw
 //     values elsewhere (masked batches that overflow the stage) are recorded and checked
 //     at the end: if the k-th best candidate is at or above the highest of them, nothing
-//     in the top k was skipped; otherwise the row is solved exactly (row_solver.hpp).
+//     in the top k was skipped; otherwise the row is solved exactly (row_solver.hpp; a
+//     min-p band that the list cannot hold, band_solver.hpp).
 //  B. Stream: raw logits are compared with the raw image of the threshold (x >= thr * T
 //     lowered by a margin is implied by z = x * (1/T) >= thr); the slots that pass are
 //     compacted into a per-wave LDS stage with ballots, then tempered, penalised if they
@@ -43,6 +44,7 @@
 #pragma once
 
 #include "args.hpp"
+#include "band_solver.hpp"
 #include "block_ops.hpp"
 #include "row_solver.hpp"
 #include "topk_path.hpp"
@@ -123,6 +125,7 @@ struct TkShared {
   uint32_t q_head;    // candidate slots the finisher has taken
   uint32_t fin_thr;   // bits of the finisher's k-th best z (-FLT_MAX until it holds k)
   int verdict;        // 1: the finisher's list is exact; 0: the row is solved exactly
+  uint32_t band_top;  // min-p band rows solved exactly: order key of the list's top (0: none)
   uint64_t queue[kTkQueue];
   SampleHist hist;    // lane maxima of every streaming wave's first batch
   SampleHist chist;   // final z of every queued candidate
@@ -144,6 +147,8 @@ struct TkLds {
   }
 };
 static_assert(sizeof(SolverShared) <= sizeof(uint64_t) * kTkStream * kTkStage, "solver scratch fits the stages");
+static_assert(band_lds_bytes(kMaxChunkLen, kTkBlock) <= sizeof(uint64_t) * kTkStream * kTkStage,
+              "the band solver's scratch of a whole-row chunk fits the stages");
 
 template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED, bool BAND>
 __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
@@ -409,7 +414,10 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       if (kth == 0ull || (uint32_t)(kth >> 32) < tm) flags |= kFlagOverflow;
     }
     exact = (flags & kFlagOverflow) && !(flags & (kFlagBadHistory | kFlagInvalid));
-    if (exact && lane == 0) s.verdict = 0;
+    if (exact && lane == 0) {
+      s.verdict = 0;
+      if constexpr (band) s.band_top = (uint32_t)(lane_get(best, 0) >> 32);  // 0: an empty list
+    }
   } else {
     // ---- A. the history ids go into the bitmap (and the count table) while the first
     // batch is in flight; once every streaming wave's are in, the final z of each lane's
@@ -729,7 +737,11 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   }
   __syncthreads();
   if (s.verdict == 0) {
-    if (INLINE) {
+    if (INLINE && BAND) {
+      // a band the list could not hold: one more pass over the row, which is still in the
+      // caches, from the list's top (the row's maximum unless candidates were lost)
+      solve_band_row<kTkBlock, DT, ALIGNED>(a, row, s.band_top, L.htab, reinterpret_cast<unsigned char*>(L.stage));
+    } else if (INLINE) {
       solve_row<kTkBlock, DT>(a, row, L.htab, *reinterpret_cast<SolverShared*>(L.stage));
     } else if (finisher && lane == 0) {
       const size_t slot = (size_t)row * (size_t)a.S + (size_t)chunk;

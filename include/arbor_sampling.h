@@ -150,8 +150,9 @@ int arbor_sample_append(const arbor_sampling_params* params, const void* logits,
  * static device scratch (ARBOR_NOALLOC_SCRATCH_BYTES per device, held from the first call
  * on a device until the process ends) serves as the workspace. Arguments and results are
  * those of arbor_sample. Params whose arbor_sample_workspace_bytes() exceeds the scratch
- * return ARBOR_ERR_WORKSPACE (streamed rows, top-k <= 64 or min-p alone, always fit; the
- * histogram solver's rows fit for small batches only). Every call on one device shares
+ * return ARBOR_ERR_WORKSPACE (every path but top-k > 64 fits at vocabularies of up to
+ * 262,144 ids, and at larger ones for batches of up to 256 rows; top-k > 64 fits for small
+ * batches only). Every call on one device shares
  * that device's scratch: calls that overlap on one device race and must be ordered (one
  * stream, or synchronised), like calls that share a workspace.
  * No counterpart in the reference: this entry point is for callers that cannot allocate

@@ -144,9 +144,9 @@ def test_workspace_bytes_configs(name):
     p = S.params_for(w)
     need = S.workspace_bytes(p)
     if name == "c2":
-        # histogram solver: one fp32 row buffer per row, plus (rows split over workgroups)
-        # one ~115 KB record per workgroup, at most one workgroup per compute unit
-        assert 0 < need <= w.batch * w.vocab * 4 + 256 * (115 << 10) + 8 * w.batch + 4096
+        # nucleus kernel, rows split over workgroups: one ~26 KB record per workgroup (at most
+        # one workgroup per compute unit) and two barrier words per row
+        assert 0 < need <= 256 * (26 << 10) + 16 * w.batch + 1024
     else:
         # streamed rows: at most the chunk lists of one workgroup per compute unit (520 B each)
         assert 0 < need <= 256 * 520 + 1024

@@ -45,9 +45,11 @@ LOOPS = [
     (4, 40000, 2, 8, 25, "f32", dict(repetition_penalty=0.8, top_p=0.7)),  # split row solver, raising penalty
     # a batch that fills the chip: one workgroup per row, the id appended by the kernel that draws it
     (256, 32000, 1, 32, 4, "f32", dict(temperature=0.7, repetition_penalty=1.15, top_k=50, top_p=0.95)),
-    # near-flat rows: the min-p band overflows the 64-entry list and the same workgroup
-    # solves each row exactly, appending from the radix solver
+    # near-flat rows: the min-p band overflows the 64-entry list and the band solver draws
+    # (one workgroup per row), appending the id itself
     (256, 4096, 1, 16, 3, "bf16", dict(min_p=0.05, repetition_penalty=1.1, _scale=0.01)),
+    # the same with rows split over workgroups: the finishing kernel's band solver appends
+    (4, 40000, 1, 16, 3, "f32", dict(min_p=0.05, repetition_penalty=1.1, _scale=0.01)),
     (300, 6000, 1, 16, 3, "f32", dict(top_k=100, _scale=0.5)),  # k > 64: the histogram solver, then an append launch
 ]
 

@@ -86,3 +86,51 @@ def test_large_shape_paths(case):
     ids_p, probs = run_gpu(S.params_for(ws), sub, write_probs=True)
     compare(S.params_for(ws), sub, ids_p, probs, label=f"{label} (probs)")
     assert np.all(ids >= 0)
+
+
+def _flat_top(inp: syn.Inputs, rows, dtype: str, width: int, seed: int) -> syn.Inputs:
+    """The given rows get a plateau: `width` random ids lifted to 4 above the row's maximum
+    (within +-0.05 of each other), so min-p's band holds far more ids than the streaming
+    kernel's 64-entry list and the row goes to the band solver."""
+    rng = np.random.default_rng(seed)
+    x = inp.logits.copy()
+    for r in rows:
+        if dtype == "bf16":
+            row = (x[r].astype(np.uint32) << 16).view(np.float32)
+        else:
+            row = x[r].copy()
+        top = float(np.max(row[np.isfinite(row)]))
+        ids = rng.choice(row.size, size=width, replace=False)
+        row[ids] = top + 4.0 + rng.uniform(-0.05, 0.05, size=width).astype(np.float32)
+        x[r] = (row.view(np.uint32) >> 16).astype(np.uint16) if dtype == "bf16" else row
+    return syn.Inputs(x, inp.history, inp.mask, inp.uniforms)
+
+
+BAND_CASES = [
+    # (label, batch, vocab, dtype, plateau width, mask) on c4's parameters (min-p 0.05 alone,
+    # frequency and presence penalties, 2048 history ids)
+    ("c4 shape, every other row flat, B=512", 512, 152064, "bf16", 400, False),
+    ("split rows (finished by the finishing kernel), B=4", 4, 152064, "bf16", 2000, False),
+    ("split rows, fp32, masked, B=3", 3, 50000, "f32", 300, True),
+    ("one row, B=1", 1, 32000, "f32", 100, False),
+]
+
+
+@pytest.mark.parametrize("case", range(len(BAND_CASES)), ids=lambda i: BAND_CASES[i][0])
+def test_band_overflow(case):
+    # flat-topped min-p rows go to the band solver, mixed with rows the 64-entry list
+    # finishes; both kinds must match the oracle
+    label, B, V, dtype, width, masked = BAND_CASES[case]
+    w = syn.CONFIGS["c4"].scaled(batch=B, vocab=V, dtype=dtype, seed=90 + case,
+                                 hist_len=min(2048, V // 8))
+    if masked:
+        w = w.scaled(mask_block_frac=0.5, mask_scatter=8)
+    print(f"[band {case}] {label}: B={B} V={V} {dtype} plateau {width}", flush=True)
+    inp = _flat_top(syn.generate(w), range(0, B, 2), dtype, width, seed=case)
+    p = S.params_for(w)
+    ids, _ = run_gpu(p, inp, repeat=2)
+    compare(S.params_for(w), inp, ids, label=label, max_boundary=max(1, B // 10))
+    assert np.all(ids >= 0)
+    if B * V <= 20_000_000:
+        ids_p, probs = run_gpu(S.params_for(w), inp, write_probs=True)
+        compare(S.params_for(w), inp, ids_p, probs, label=f"{label} (probs)")
