@@ -29,6 +29,7 @@
 #include "../../include/arbor_sampling.h"
 #include "args.hpp"
 #include "block_ops.hpp"
+#include "lm_head.hpp"
 #include "mass_solver.hpp"
 #include "nucleus.hpp"
 #include "row_solver.hpp"
@@ -731,6 +732,110 @@ int arbor_embed(const int32_t* ids, int32_t count, const void* table, int32_t vo
     hipLaunchKernelGGL(arbor::embed_kernel<false>, grid, dim3(256), 0, s, ids, tb, (int)vocab, (int)row_bytes, ob);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? ARBOR_OK : hip_fail(e, "kernel launch");
+}
+
+size_t arbor_lm_head_packed_bytes(int32_t hidden, int32_t vocab) {
+  if (hidden <= 0 || hidden % arbor::kLmHidden != 0 || vocab <= 0 || vocab > ARBOR_VOCAB_MAX) return 0;
+  return arbor::lm_packed_bytes(hidden, vocab);
+}
+
+int arbor_lm_head_pack(const void* weight, int32_t weight_dtype, int32_t layout, int32_t hidden, int32_t vocab,
+                       void* packed, void* stream) {
+  if (arbor_lm_head_packed_bytes(hidden, vocab) == 0)
+    return fail(ARBOR_ERR_SHAPE, "hidden %d must be a positive multiple of %d and vocab %d in (0, %d]", hidden,
+                arbor::kLmHidden, vocab, ARBOR_VOCAB_MAX);
+  if (weight_dtype != ARBOR_DTYPE_F32 && weight_dtype != ARBOR_DTYPE_BF16)
+    return fail(ARBOR_ERR_DTYPE, "unknown weight dtype %d", weight_dtype);
+  if (layout != ARBOR_LM_WEIGHT_HV && layout != ARBOR_LM_WEIGHT_VH)
+    return fail(ARBOR_ERR_FLAGS, "unknown weight layout %d", layout);
+  if (!weight || !packed) return fail(ARBOR_ERR_NULL, "weight and packed are required");
+  if ((uintptr_t)packed % 16 != 0) return fail(ARBOR_ERR_SHAPE, "packed must be 16-byte aligned");
+  const int rows = (int)((vocab + arbor::kLmRows - 1) / arbor::kLmRows * arbor::kLmRows);
+  const size_t units = (size_t)rows * (size_t)(hidden / 8);
+  const dim3 grid((unsigned)((units + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  arbor::lm_u4* out = static_cast<arbor::lm_u4*>(packed);
+  if (weight_dtype == ARBOR_DTYPE_F32)
+    hipLaunchKernelGGL(arbor::lm_pack_kernel<ARBOR_DTYPE_F32>, grid, dim3(256), 0, s, weight, (int)layout, (int)hidden,
+                       (int)vocab, rows, out);
+  else
+    hipLaunchKernelGGL(arbor::lm_pack_kernel<ARBOR_DTYPE_BF16>, grid, dim3(256), 0, s, weight, (int)layout, (int)hidden,
+                       (int)vocab, rows, out);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ARBOR_OK : hip_fail(e, "kernel launch");
+}
+
+}  // extern "C"
+
+namespace {
+template <int NT, int XDT>
+void launch_lm_nt(const arbor::LmArgs& a, int odt, hipStream_t s) {
+  const dim3 grid((unsigned)((a.V + arbor::kLmRows - 1) / arbor::kLmRows)), block(arbor::kLmThreads);
+  if (odt == ARBOR_DTYPE_F32)
+    hipLaunchKernelGGL((arbor::lm_head_kernel<NT, XDT, ARBOR_DTYPE_F32>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((arbor::lm_head_kernel<NT, XDT, ARBOR_DTYPE_BF16>), grid, block, 0, s, a);
+}
+template <int XDT>
+void launch_lm(const arbor::LmArgs& a, int odt, hipStream_t s) {
+  // batch rows in N-tiles of 32: 1, 2, 4 or 8 tiles
+  const int nt = (a.B + 31) / 32;
+  if (nt <= 1) launch_lm_nt<1, XDT>(a, odt, s);
+  else if (nt <= 2) launch_lm_nt<2, XDT>(a, odt, s);
+  else if (nt <= 4) launch_lm_nt<4, XDT>(a, odt, s);
+  else launch_lm_nt<8, XDT>(a, odt, s);
+}
+}  // namespace
+
+extern "C" {
+
+int arbor_lm_head(const void* x, int32_t x_dtype, int32_t batch, int32_t ld_x, const void* packed, const float* bias,
+                  int32_t hidden, int32_t vocab, float scale, void* logits, int32_t logits_dtype, int32_t ld_logits,
+                  float* row_max, void* stream) {
+  if (arbor_lm_head_packed_bytes(hidden, vocab) == 0)
+    return fail(ARBOR_ERR_SHAPE, "hidden %d must be a positive multiple of %d and vocab %d in (0, %d]", hidden,
+                arbor::kLmHidden, vocab, ARBOR_VOCAB_MAX);
+  if (batch < 0 || ld_x < hidden || ld_logits < vocab)
+    return fail(ARBOR_ERR_SHAPE, "batch %d >= 0, ld_x %d >= hidden %d and ld_logits %d >= vocab %d are required", batch,
+                ld_x, hidden, ld_logits, vocab);
+  if ((x_dtype != ARBOR_DTYPE_F32 && x_dtype != ARBOR_DTYPE_BF16) ||
+      (logits_dtype != ARBOR_DTYPE_F32 && logits_dtype != ARBOR_DTYPE_BF16))
+    return fail(ARBOR_ERR_DTYPE, "unknown dtype: x %d, logits %d", x_dtype, logits_dtype);
+  if (!std::isfinite(scale)) return fail(ARBOR_ERR_TEMPERATURE, "scale must be finite, got %g", (double)scale);
+  if (batch == 0) return ARBOR_OK;
+  if (!x || !packed || !logits) return fail(ARBOR_ERR_NULL, "x, packed and logits are required");
+  const size_t xe = x_dtype == ARBOR_DTYPE_BF16 ? 2 : 4;
+  if ((uintptr_t)x % 16 != 0 || ((size_t)ld_x * xe) % 16 != 0 || (uintptr_t)packed % 16 != 0)
+    return fail(ARBOR_ERR_SHAPE, "x rows (ld_x %d) and packed must be 16-byte aligned", ld_x);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (row_max) {
+    hipLaunchKernelGGL(arbor::lm_fill_kernel, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s, row_max,
+                       (int)batch, -INFINITY);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  }
+  const size_t oe = logits_dtype == ARBOR_DTYPE_BF16 ? 2 : 4;
+  for (int b0 = 0; b0 < batch; b0 += arbor::kLmMaxB) {
+    arbor::LmArgs a{};
+    a.x = static_cast<const char*>(x) + (size_t)b0 * (size_t)ld_x * xe;
+    a.ld_x = ld_x;
+    a.w = static_cast<const arbor::lm_u4*>(packed);
+    a.bias = bias;
+    a.out = static_cast<char*>(logits) + (size_t)b0 * (size_t)ld_logits * oe;
+    a.ld_out = ld_logits;
+    a.row_max = row_max ? row_max + b0 : nullptr;
+    a.scale = scale;
+    a.B = batch - b0 < arbor::kLmMaxB ? batch - b0 : arbor::kLmMaxB;
+    a.H = hidden;
+    a.V = vocab;
+    if (x_dtype == ARBOR_DTYPE_BF16)
+      launch_lm<ARBOR_DTYPE_BF16>(a, logits_dtype, s);
+    else
+      launch_lm<ARBOR_DTYPE_F32>(a, logits_dtype, s);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  }
+  return ARBOR_OK;
 }
 
 int arbor_device_count(int* count) {

@@ -43,6 +43,8 @@ namespace ArborNet.Core.Native.PInvoke
         public const uint ARBOR_FLAG_WRITE_PROBS = 1;
         public const int ARBOR_VOCAB_MAX = 1048575;
         public const int ARBOR_HISTORY_MAX = 4096;
+        public const int ARBOR_LM_WEIGHT_HV = 0;  // [hidden, vocab]: Linear.weight (in x out)
+        public const int ARBOR_LM_WEIGHT_VH = 1;  // [vocab, hidden]
 
         public const int ARBOR_OK = 0;
         public const int ARBOR_ERR_NULL = -1;
@@ -124,6 +126,20 @@ namespace ArborNet.Core.Native.PInvoke
         [DllImport(Lib, CallingConvention = CallingConvention.Cdecl)]
         public static extern int arbor_embed(IntPtr ids, int count, IntPtr table, int vocab, int width, int dtype,
             IntPtr outRows, IntPtr stream);
+
+        // The LM head before the sampler: logits = (x . W + bias) * scale on the matrix cores,
+        // the product Linear.Forward computes as input.MatMul(weight).Add(bias) (Linear.cs:29).
+        [DllImport(Lib, CallingConvention = CallingConvention.Cdecl)]
+        public static extern UIntPtr arbor_lm_head_packed_bytes(int hidden, int vocab);
+
+        [DllImport(Lib, CallingConvention = CallingConvention.Cdecl)]
+        public static extern int arbor_lm_head_pack(IntPtr weight, int weightDtype, int layout, int hidden, int vocab,
+            IntPtr packed, IntPtr stream);
+
+        [DllImport(Lib, CallingConvention = CallingConvention.Cdecl)]
+        public static extern int arbor_lm_head(IntPtr x, int xDtype, int batch, int ldX, IntPtr packed, IntPtr bias,
+            int hidden, int vocab, float scale, IntPtr logits, int logitsDtype, int ldLogits, IntPtr rowMax,
+            IntPtr stream);
 
         /// <summary>True when the library loads and sees a HIP device (CUDA.IsAvailable's role).</summary>
         public static bool IsAvailable()

@@ -31,6 +31,7 @@ ARBOR_ID_EMPTY = -1
 ARBOR_ID_INVALID = -2
 ARBOR_ID_BAD_HISTORY = -3
 ARBOR_ID_STALLED = -4
+ARBOR_VOCAB_MAX = 1048575
 
 STATUS_NAMES = {
     0: "ARBOR_OK",
@@ -126,6 +127,13 @@ def library() -> ctypes.CDLL:
         lib.arbor_decode.restype = i32
         lib.arbor_embed.argtypes = [vp, ctypes.c_int32, vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, vp, vp]
         lib.arbor_embed.restype = i32
+        lib.arbor_lm_head_packed_bytes.argtypes = [ctypes.c_int32, ctypes.c_int32]
+        lib.arbor_lm_head_packed_bytes.restype = sz
+        lib.arbor_lm_head_pack.argtypes = [vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, vp, vp]
+        lib.arbor_lm_head_pack.restype = i32
+        lib.arbor_lm_head.argtypes = [vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, vp, vp, ctypes.c_int32,
+                                      ctypes.c_int32, ctypes.c_float, vp, ctypes.c_int32, ctypes.c_int32, vp, vp]
+        lib.arbor_lm_head.restype = i32
         lib.arbor_sample_noalloc.argtypes = [P, vp, vp, vp, vp, vp, vp, vp]
         lib.arbor_sample_noalloc.restype = i32
         lib.arbor_sample_workspace_bytes.argtypes = [P]
@@ -414,3 +422,63 @@ def embed(ids, table, out=None):
     check(int(library().arbor_embed(ids.data_ptr(), ids.numel(), table.data_ptr(), table.shape[0], table.shape[1],
                                     dtype, out.data_ptr(), stream)))
     return out
+
+
+ARBOR_LM_WEIGHT_HV = 0  # weight [hidden, vocab]: the reference's Linear.weight (in x out)
+ARBOR_LM_WEIGHT_VH = 1  # weight [vocab, hidden]
+
+
+def _dtype_code(t):
+    import torch
+
+    code = {torch.float32: ARBOR_DTYPE_F32, torch.bfloat16: ARBOR_DTYPE_BF16}.get(t.dtype)
+    if code is None:
+        raise ArborSamplingError(-4, f"dtype {t.dtype} is not float32 or bfloat16")
+    return code
+
+
+class LMHead:
+    """The logits producer before the sampler, on the matrix cores: logits = (x @ W + bias)
+    * scale with bf16 operands and fp32 accumulation (arbor_lm_head). Mirrors the reference's
+    Linear.Forward, input.MatMul(weight).Add(bias) (ArborNet.Layers/Linear.cs:29), whose weight
+    is [in, out] = [hidden, vocab] (layout "hv"); "vh" takes a [vocab, hidden] weight. The
+    weight is packed once, here, into the order the matrix instructions read."""
+
+    def __init__(self, weight, bias=None, layout: str = "hv"):
+        import torch
+
+        if weight.dim() != 2 or not weight.is_contiguous():
+            raise ValueError("weight must be a contiguous 2-D tensor")
+        lay = {"hv": ARBOR_LM_WEIGHT_HV, "vh": ARBOR_LM_WEIGHT_VH}[layout]
+        self.hidden, self.vocab = (weight.shape[0], weight.shape[1]) if lay == ARBOR_LM_WEIGHT_HV else \
+            (weight.shape[1], weight.shape[0])
+        self.device = weight.device
+        nbytes = int(library().arbor_lm_head_packed_bytes(self.hidden, self.vocab))
+        if nbytes == 0:
+            raise ArborSamplingError(-3, f"hidden {self.hidden} must be a positive multiple of 128, vocab {self.vocab} "
+                                         f"in (0, {ARBOR_VOCAB_MAX}]")
+        self.packed = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        check(int(library().arbor_lm_head_pack(weight.data_ptr(), _dtype_code(weight), lay, self.hidden, self.vocab,
+                                               self.packed.data_ptr(), stream)))
+        self.bias = None if bias is None else bias.to(device=self.device, dtype=torch.float32).contiguous()
+
+    def __call__(self, x, scale: float = 1.0, out_dtype=None, out=None, row_max: bool = False):
+        """x [batch, hidden] (rows may be strided) -> logits [batch, vocab] (fp32 unless
+        out_dtype or out says bf16), and the rows' maxima if row_max."""
+        import torch
+
+        if x.dim() != 2 or x.shape[1] != self.hidden or x.stride(1) != 1:
+            raise ValueError(f"x must be [batch, {self.hidden}] with unit column stride")
+        B = x.shape[0]
+        if out is None:
+            out = torch.empty((B, self.vocab), dtype=out_dtype or torch.float32, device=self.device)
+        if out.dim() != 2 or out.shape[0] != B or out.shape[1] < self.vocab or out.stride(1) != 1:
+            raise ValueError("out must be [batch, >= vocab] with unit column stride")
+        rm = torch.empty(B, dtype=torch.float32, device=self.device) if row_max else None
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        check(int(library().arbor_lm_head(
+            x.data_ptr(), _dtype_code(x), B, x.stride(0), self.packed.data_ptr(),
+            None if self.bias is None else self.bias.data_ptr(), self.hidden, self.vocab, float(scale),
+            out.data_ptr(), _dtype_code(out), out.stride(0), None if rm is None else rm.data_ptr(), stream)))
+        return (out, rm) if row_max else out

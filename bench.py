@@ -50,6 +50,10 @@ def parse():
                     help="time the generation step (arbor_sample_append: sample, then append the ids to the "
                          "row's history ring) instead of arbor_sample; needs a workload with history")
     ap.add_argument("--sets", type=int, default=0, help="input sets rotated (0 = auto)")
+    ap.add_argument("--lm-head", action="store_true",
+                    help="time the LM head before the sampler (arbor_lm_head: bf16 [B, H] x packed bf16 "
+                         "[H, V] weight + bias -> fp32 logits) at B=256, V=128256 and --lm-hidden")
+    ap.add_argument("--lm-hidden", type=int, default=4096)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="bytes of the device-to-device copy that gives the practical ceiling and "
                          "calibrates the rocprofv3 counters (default: one input set)")
@@ -78,6 +82,101 @@ def traffic_from_profiles(cfg: str):
         return None
 
 
+def bench_lm_head(args):
+    """One JSON line for the LM head: a step is one arbor_lm_head call producing the fp32
+    logits of a batch (B=256, H=--lm-hidden, V=128256: c3's batch and vocabulary) from bf16
+    hidden states and the packed bf16 weight, bias added. The weight (2·H·V bytes) is read
+    once per call, so the roofline is HBM: algorithmic bytes = weight + x + bias + logits."""
+    import torch
+
+    from arbornet_amd import sampling as S
+
+    B, H, V = 256, args.lm_hidden, 128256
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    w = (torch.randn((H, V), device=dev, generator=g) / H ** 0.5).to(torch.bfloat16)  # [hidden, vocab]
+    bias = torch.randn(V, device=dev, generator=g) * 0.1
+    head = S.LMHead(w, bias, layout="hv")
+    x = torch.randn((B, H), device=dev, generator=g).to(torch.bfloat16)
+    out = torch.empty((B, V), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        head(x, out=out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall1 = time.perf_counter()
+    ms = e0.elapsed_time(e1) / args.steps
+    # practical reference point: torch's bf16 GEMM of the same operands (hipBLASLt; bf16
+    # output, no bias), contiguous [B, H] @ [H, V]
+    for _ in range(20):
+        torch.matmul(x, w)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        torch.matmul(x, w)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    mm_ms = e0.elapsed_time(e1) / args.steps
+    wbytes = int(head.packed.numel())
+    nbytes = wbytes + B * H * 2 + V * 4 + B * V * 4
+    flops = 2.0 * B * H * V
+    gbs = nbytes / (ms / 1e3) / 1e9
+    tflops = flops / (ms / 1e3) / 1e12
+    cpu = None
+    if not args.no_cpu_baseline:
+        # numpy fp32 GEMM (threaded BLAS) of the reference's product on a column sample
+        cols = 4096
+        xh = x.float().cpu().numpy()
+        wh = w[:, :cols].float().cpu().numpy()
+        bh = bias[:cols].cpu().numpy()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < max(1.0, args.cpu_seconds / 2):
+            _ = xh @ wh + bh
+            n += 1
+        el = time.perf_counter() - t0
+        thr = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        cpu = {
+            "value": round(B * n / el * cols / V, 1), "unit": "rows/s", "cores": thr, "kind": "port",
+            "sample": f"numpy fp32 x[{B},{H}] @ W[{H},{cols}] + bias, {n} times in {el:.1f} s, scaled to V={V} "
+                      f"({cpu_model()})",
+        }
+    out_line = {
+        "metric": f"LM-head logits rows/sec at B={B}, H={H}, V={V} (bf16 operands, fp32 logits + bias)",
+        "value": round(B / (ms / 1e3), 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"lm_head: B={B} H={H} V={V}, weight [H, V] bf16 packed, fp32 logits",
+                   "wall_s_timed": round(wall1 - wall0, 4)},
+        "roofline": {
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": nbytes,
+            "mfma_tflops": round(tflops, 1), "mfma_frac": round(tflops / 2500.0, 4),
+            "torch_bf16_mm_ms": round(mm_ms, 5),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out_line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -94,6 +193,9 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     S.library()
+    if args.lm_head:
+        bench_lm_head(args)
+        return
     w = syn.CONFIGS[args.config]
     dev = torch.device("cuda:0")
     inp = syn.generate(w)

@@ -192,6 +192,38 @@ int arbor_decode(const int32_t* ids, int32_t count, const int32_t* token_offsets
 int arbor_embed(const int32_t* ids, int32_t count, const void* table, int32_t vocab, int32_t width, int32_t dtype,
                 void* out_rows, void* stream);
 
+/*
+ * The LM head, the step before the sampler: logits = (x · W + bias) · scale, the product
+ * the reference computes as input.MatMul(weight).Add(bias) (ArborNet.Layers/Linear.cs:29,
+ * on kernel.cu:56-64 matmul_kernel or hipBLAS sgemm, ArborNet.Core/Native/PInvoke/
+ * ROCm.cs:224-229), on the matrix cores: operands rounded to bf16 (round to nearest even),
+ * products accumulated in fp32, then + bias and × scale in fp32 (scale = 1 keeps the
+ * sampler's temperature separate; scale = 1/T with the sampler at temperature 1 folds it
+ * in), stored as fp32 or bf16.
+ *
+ * The weight is packed once (at load time) into the order the matrix instructions read:
+ *   arbor_lm_head_packed_bytes  bytes of the packed weight (0 if hidden is not a positive
+ *                               multiple of 128 or vocab is not in (0, ARBOR_VOCAB_MAX])
+ *   arbor_lm_head_pack          weight [hidden, vocab] (ARBOR_LM_WEIGHT_HV, the reference's
+ *                               Linear.weight layout, in x out, Linear.cs:14-18) or
+ *                               [vocab, hidden] (ARBOR_LM_WEIGHT_VH) row-major, fp32 or bf16
+ *                               -> packed (device, arbor_lm_head_packed_bytes bytes)
+ *   arbor_lm_head               x [batch, ld_x] (fp32 or bf16; 16-byte aligned rows) ->
+ *                               logits [batch, ld_logits] (fp32 or bf16); bias [vocab] fp32
+ *                               or NULL; row_max [batch] fp32 or NULL: each row's largest
+ *                               stored logit (NaN ignored). Any batch; the weight is read
+ *                               once per 256 rows.
+ * These allocate nothing; they run on `stream` and return once launched.
+ */
+#define ARBOR_LM_WEIGHT_HV 0 /* [hidden, vocab]: the reference's Linear.weight */
+#define ARBOR_LM_WEIGHT_VH 1 /* [vocab, hidden] */
+size_t arbor_lm_head_packed_bytes(int32_t hidden, int32_t vocab);
+int arbor_lm_head_pack(const void* weight, int32_t weight_dtype, int32_t layout, int32_t hidden,
+                       int32_t vocab, void* packed, void* stream);
+int arbor_lm_head(const void* x, int32_t x_dtype, int32_t batch, int32_t ld_x, const void* packed,
+                  const float* bias, int32_t hidden, int32_t vocab, float scale, void* logits,
+                  int32_t logits_dtype, int32_t ld_logits, float* row_max, void* stream);
+
 /* Bytes of workspace arbor_sample needs for these params (0 if params are invalid).
  * No reference counterpart: the reference's kernels need no scratch (CudaBackend.cs:43-46). */
 size_t arbor_sample_workspace_bytes(const arbor_sampling_params* params);

@@ -215,3 +215,22 @@ def test_sample_append_argument_checks():
     assert S.sample_append_raw(r, 16, 16, 16, None, 16, 16, None, 16, 1 << 30, None) == -8
     assert lib.arbor_sample_append(None, 16, 16, 16, None, 16, 16, None, 16, 1 << 30, None) == -1
     assert b"history" in lib.arbor_last_error() or lib.arbor_last_error()
+
+
+def test_lm_head_arguments_checked_on_the_host():
+    # the LM head's shape, dtype and layout rules, checked before anything is launched
+    lib = S.library()
+    assert lib.arbor_lm_head_packed_bytes(4096, 128256) == ((128256 + 255) // 256 * 256) * 4096 * 2
+    assert lib.arbor_lm_head_packed_bytes(100, 1000) == 0        # hidden not a multiple of 128
+    assert lib.arbor_lm_head_packed_bytes(128, 0) == 0
+    assert lib.arbor_lm_head_packed_bytes(128, S.ARBOR_VOCAB_MAX + 1) == 0
+    assert lib.arbor_lm_head_pack(16, 0, 0, 100, 1000, 16, None) == -3      # ARBOR_ERR_SHAPE
+    assert lib.arbor_lm_head_pack(16, 7, 0, 128, 1000, 16, None) == -4      # ARBOR_ERR_DTYPE
+    assert lib.arbor_lm_head_pack(16, 0, 2, 128, 1000, 16, None) == -13     # unknown layout
+    assert lib.arbor_lm_head_pack(None, 0, 0, 128, 1000, 16, None) == -1    # ARBOR_ERR_NULL
+    assert lib.arbor_lm_head(16, 1, 4, 120, 16, None, 128, 1000, 1.0, 16, 0, 1000, None, None) == -3  # ld_x < hidden
+    assert lib.arbor_lm_head(16, 1, 4, 128, 16, None, 128, 1000, 1.0, 16, 3, 1000, None, None) == -4  # logits dtype
+    assert lib.arbor_lm_head(16, 1, 4, 128, 16, None, 128, 1000, float("inf"), 16, 0, 1000, None, None) == -5
+    assert lib.arbor_lm_head(None, 1, 4, 128, 16, None, 128, 1000, 1.0, 16, 0, 1000, None, None) == -1
+    assert lib.arbor_lm_head(8, 1, 4, 128, 16, None, 128, 1000, 1.0, 16, 0, 1000, None, None) == -3  # x not 16-byte aligned
+    assert lib.arbor_lm_head(None, 1, 0, 128, None, None, 128, 1000, 1.0, None, 0, 1000, None, None) == 0  # empty batch

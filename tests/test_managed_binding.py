@@ -55,7 +55,7 @@ def c_to_cs(c: str, *, ret: bool = False) -> set[str]:
     """The marshalling types a C# declaration may use for a C type."""
     c = c.replace("const ", "")
     table = {
-        "int": {"int"}, "int32_t": {"int"}, "uint32_t": {"uint"}, "size_t": {"UIntPtr", "nuint"},
+        "int": {"int"}, "int32_t": {"int"}, "uint32_t": {"uint"}, "size_t": {"UIntPtr", "nuint"}, "float": {"float"},
         "void": {"void"}, "char *": {"IntPtr"},
         "arbor_sampling_params *": {"ref ArborSamplingParams", "out ArborSamplingParams"},
         "int *": {"out int", "IntPtr"}, "void * *": {"out IntPtr"},
