@@ -60,10 +60,23 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
   __shared__ SolverShared ssh;
   __shared__ uint32_t s_flags;
   const int lane = lane_id(), row = blockIdx.x;
-  if (threadIdx.x == 0) {
+  // wave 0 requests every chunk's count, flags and 64 list slots in one round (slots past
+  // a chunk's count hold stale keys and are masked once the counts are in)
+  constexpr int kGroup = 8;  // chunks merged per round of loads
+  uint64_t v0[kGroup];
+  uint32_t n0 = 0u;
+  if (threadIdx.x < kWave) {
     uint32_t f = 0u;
-    for (int c = 0; c < a.S; ++c) f |= a.hdr[((size_t)row * (size_t)a.S + (size_t)c) * 2 + 1];
-    s_flags = f;
+    if (lane < a.S) {
+      const size_t slot = (size_t)row * (size_t)a.S + (size_t)lane;
+      n0 = a.hdr[slot * 2 + 0];
+      f = a.hdr[slot * 2 + 1];
+    }
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j)
+      v0[j] = j < a.S ? a.cand[((size_t)row * (size_t)a.S + (size_t)j) * kChunkSlot + lane] : 0ull;
+    f = wave_reduce(f, [](uint32_t x, uint32_t y) { return x | y; });
+    if (lane == 0) s_flags = f;
   }
   __syncthreads();
   const uint32_t flags = s_flags;
@@ -88,10 +101,14 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
   __shared__ int s_exact;
   uint64_t best = 0ull;
   if (threadIdx.x < kWave) {
-    for (int cb = 0; cb < a.S; cb += 8) {
-      uint64_t v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < kGroup; ++j)
+      if (j < a.S) best = list_merge(best, lane < (int)lane_get(n0, j) ? v0[j] : 0ull);
+    // more than kGroup chunks (rows of more than 8 chunks): the rest, kGroup at a time
+    for (int cb = kGroup; cb < a.S; cb += kGroup) {
+      uint64_t v[kGroup];
+#pragma unroll
+      for (int j = 0; j < kGroup; ++j) {
         const int c = cb + j;
         v[j] = 0ull;
         if (c < a.S) {
@@ -101,7 +118,7 @@ __global__ void __launch_bounds__(kBlock) topk_finish_kernel(Args a) {
         }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < kGroup; ++j)
         if (cb + j < a.S) best = list_merge(best, v[j]);
     }
     const uint64_t last = lane_get(best, kWave - 1), top = lane_get(best, 0);
