@@ -327,4 +327,64 @@ __device__ __forceinline__ void solve_band_row(const Args& a, int row, uint32_t 
   }
 }
 
+// LDS of draw_band_candidates: ids, masses and ids in id order (BLOCK each) and the
+// block reductions' scratch.
+template <int BLOCK>
+__host__ __device__ constexpr size_t band_draw_lds_bytes() {
+  return 3 * sizeof(uint32_t) * BLOCK + (sizeof(double) + sizeof(int32_t)) * (BLOCK / kWave);
+}
+
+// Min-p draw over a row's candidates when every id of the band is among them: cand[0, n)
+// (n <= BLOCK) holds final-z composites of distinct ids, top_key is the order key of the
+// row's maximum z, and the row's probabilities are zero where the draw writes none. Band
+// membership and masses are those of solve_band_row; each member's place in id order is
+// the count of members with smaller ids, and the masses, placed in that order, are summed
+// by one block scan, so the result does not depend on the candidates' order.
+template <int BLOCK>
+__device__ __forceinline__ void draw_band_candidates(const Args& a, int row, const uint64_t* cand, int n, uint32_t top_key, float u,
+                                     unsigned char* lds) {
+  uint32_t* ids = reinterpret_cast<uint32_t*>(lds);  // [BLOCK] member ids, 0xFFFFFFFF elsewhere
+  float* es = reinterpret_cast<float*>(ids + BLOCK);  // [BLOCK] masses in id order
+  int32_t* sid = reinterpret_cast<int32_t*>(es + BLOCK);  // [BLOCK] ids in id order
+  double* red_d = reinterpret_cast<double*>(sid + BLOCK);
+  int32_t* red_i = reinterpret_cast<int32_t*>(red_d + BLOCK / kWave);
+  const int t = threadIdx.x;
+  const float zh = key_value(top_key);
+  const double zhd = (double)zh;
+  const float thr = zh + a.ln_min_p_lo;
+  const uint64_t c = t < n ? cand[t] : 0ull;
+  const float z = composite_z(c);
+  const int32_t id = composite_id(c);
+  const bool in = c != 0ull && z >= thr && (double)z - zhd >= a.ln_min_p;
+  ids[t] = in ? (uint32_t)id : 0xFFFFFFFFu;
+  const int nb = block_reduce_sum<BLOCK, int32_t>(in ? 1 : 0, red_i);  // its barriers publish ids
+  const float e = in ? rel_exp(z, zh) : 0.0f;
+  if (in) {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    const u4* v = reinterpret_cast<const u4*>(ids);
+    const uint32_t me = (uint32_t)id;
+    int rank = 0;
+    for (int j = 0; j < (n + 3) / 4; ++j) {
+      const u4 w = v[j];
+      rank += (w.x < me ? 1 : 0) + (w.y < me ? 1 : 0) + (w.z < me ? 1 : 0) + (w.w < me ? 1 : 0);
+    }
+    es[rank] = e;
+    sid[rank] = id;
+  }
+  __syncthreads();
+  const double ev = t < nb ? (double)es[t] : 0.0;
+  double E;
+  const double incl = block_scan_excl<BLOCK, double>(ev, red_d, &E) + ev;
+  const double target = (double)u * E;
+  // the first member in id order whose running mass passes u * E (none through rounding at
+  // u -> 1: the last member)
+  const int first = block_reduce_min<BLOCK, int32_t>(t < nb && incl > target ? t : BLOCK, red_i);
+  if (t == 0) {
+    const int32_t pick = sid[first < nb ? first : nb - 1];
+    a.out_ids[row] = pick;
+    ring_append(a, row, pick);
+  }
+  if (a.write_probs && in) a.out_probs[(size_t)row * (size_t)a.V + id] = (float)((double)e / E);
+}
+
 }  // namespace arbor

@@ -37,6 +37,15 @@
 //     each batch. After the last streaming wave it draws in fp64 (topk_path.hpp), or
 //     publishes the chunk's list for topk_finish_kernel.
 //
+// Min-p as the only filter (band rows): the kept set is every id with z >= zmax +
+// ln(min_p), so the thresholds are edges of that band instead of k-th bests: the largest
+// final z sampled or queued so far (an LDS maximum), plus ln(min_p) lowered by a margin.
+// The finisher keeps the 64 best in its list; a row finished here spills to LDS what leaves
+// the list while it is still inside the band of the best z then known (up to kTkSpill
+// entries), and when the final band reaches into the spill the whole workgroup draws over
+// list and spill (draw_band_candidates). A spill that overflows, or a split row whose list
+// cannot hold its band, goes to the band solver's pass over the row.
+//
 // History ids: when no penalty can raise a logit (repetition >= 1, frequency and presence
 // >= 0) an id's penalised z is at most its raw z, so the raw test is enough and history
 // ids are penalised when they pass it. Otherwise they are dropped from the stream and the
@@ -58,6 +67,7 @@ constexpr int kTkStage = 128;               // raw candidates of one batch stage
 constexpr int kTkQueue = 1024;              // candidate ring between the streamers and the finisher
 constexpr int kSampleBits = 12;             // threshold histogram: top 12 bits of the order key
 constexpr int kSampleBins = 1 << kSampleBits;
+constexpr int kTkSpill = 960;               // min-p band entries the finisher may spill (+ 64 in its list)
 constexpr int kBufferWord3 = 0x00020000;    // buffer resource word 3 (gfx9 family: 32-bit data format)
 constexpr int kBufferNt = 2;                // buffer load cache policy: non-temporal
 static_assert((kTkQueue & (kTkQueue - 1)) == 0, "the ring size is a power of two");
@@ -124,11 +134,19 @@ struct TkShared {
   uint32_t q_tail;    // candidate slots reserved in the ring
   uint32_t q_head;    // candidate slots the finisher has taken
   uint32_t fin_thr;   // bits of the finisher's k-th best z (-FLT_MAX until it holds k)
-  int verdict;        // 1: the finisher's list is exact; 0: the row is solved exactly
-  uint32_t band_top;  // min-p band rows solved exactly: order key of the list's top (0: none)
+  int verdict;        // 1: the finisher's list is exact; 0: the row is solved exactly;
+                      // 2: a min-p band row drawn over its list and its spilled entries
+  uint32_t band_top;  // min-p band rows: order key of the list's top (0: none)
+  uint32_t qtop;      // min-p band rows: order key of the largest final z sampled or queued
+  int spill_n;        // min-p band rows drawn over list and spill: entries in `spill`
   uint64_t queue[kTkQueue];
   SampleHist hist;    // lane maxima of every streaming wave's first batch
-  SampleHist chist;   // final z of every queued candidate
+  union {
+    SampleHist chist;  // final z of every queued candidate
+    // min-p band rows, which use no candidate histogram: candidates the finisher's list
+    // dropped while they were still inside the band of the best z then known
+    uint64_t spill[kTkSpill + kWave];
+  };
 };
 
 // Dynamic LDS of topk_kernel: staged raw candidates | chunk bitmap | history table;
@@ -147,6 +165,9 @@ struct TkLds {
   }
 };
 static_assert(sizeof(SolverShared) <= sizeof(uint64_t) * kTkStream * kTkStage, "solver scratch fits the stages");
+static_assert(band_draw_lds_bytes<kTkBlock>() <= sizeof(uint64_t) * kTkStream * kTkStage,
+              "the band draw's scratch fits the stages");
+static_assert(kTkSpill + kWave <= kTkBlock, "a band draw takes one candidate per thread");
 static_assert(band_lds_bytes(kMaxChunkLen, kTkBlock) <= sizeof(uint64_t) * kTkStream * kTkStage,
               "the band solver's scratch of a whole-row chunk fits the stages");
 
@@ -195,6 +216,8 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   // must hold every id of the band z >= zmax + ln(min_p); ln_lo is that bound's
   // safety-margined log
   constexpr bool band = BAND;
+  // band rows finished here: entries the list drops inside the band go to an LDS spill
+  constexpr bool SPILL = BAND && INLINE;
   const int k = band ? kWave : a.top_k;
   const float ln_lo = a.ln_min_p_lo;
 
@@ -316,6 +339,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     s.q_head = 0u;
     s.fin_thr = __float_as_uint(-FLT_MAX);
     s.verdict = 1;
+    s.qtop = 0u;
   }
   for (int i = t; i < kTkQueue; i += kTkBlock) s.queue[i] = 0ull;
   for (int i = t; i < (int)(sizeof(s.hist) / 4); i += kTkBlock) {
@@ -335,11 +359,21 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
 
   uint64_t best = 0ull;  // the finisher's list: the chunk's best 64 candidates, lane i = i-th
   uint32_t flags = 0u;
-  bool exact = false;  // the finisher's verdict: the row must be solved exactly
+  bool exact = false;  // the finisher's verdict: the row is not drawn from its list alone
   if (finisher) {
     // ---- C. the finisher ----
     uint32_t head = 0u;
     float pub = -FLT_MAX;
+    int nsp = 0;  // entries spilled (more than kTkSpill: the spill overflowed)
+    // the lanes' entries (0: none) at or above `edge` go to the spill
+    auto spill = [&](uint64_t d, float edge) {
+      const bool sp = d != 0ull && composite_z(d) >= edge;
+      const uint64_t m = __ballot(sp);
+      if (!m) return;
+      const int p = nsp + lanes_below(m);
+      if (sp && p < kTkSpill) s.spill[p] = d;
+      nsp += __popcll(m);
+    };
     for (;;) {
       const uint32_t tail = __atomic_load_n(&s.q_tail, __ATOMIC_RELAXED);
       if (tail == head) {
@@ -366,28 +400,51 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       wave_lds_sync();
       if (lane == 0) __atomic_store_n(&s.q_head, head, __ATOMIC_RELAXED);
       // entries below the list's k-th cannot enter the top k (the streaming waves see the
-      // k-th late); the rest are inserted one by one when few, else sorted and merged
+      // k-th late); the rest are inserted one by one when few, else sorted and merged.
+      // Band rows drawn here keep what leaves the list while it is inside the band of the
+      // best z so far (lane i of `out`: the i-th entry pushed out by an insertion, or the
+      // merge's lower half; `c` where it did not enter).
       {
         const uint64_t kth0 = lane_get(best, k - 1);
         const bool keep = c != 0ull && c > kth0;
         const uint64_t km = __ballot(keep);
         const int nk = __popcll(km);
+        uint64_t out = 0ull;
         if (nk > 0 && nk <= 8) {
           uint64_t rest = km;
+          int nout = 0;
           while (rest) {
             const int src = __ffsll((long long)rest) - 1;
             rest &= rest - 1;
-            best = list_insert(best, lane_get(c, src));
+            const uint64_t ci = lane_get(c, src);
+            if (SPILL) {
+              // the list's last entry leaves it, or the candidate itself when earlier ones
+              // of this batch have lifted the last above it
+              const uint64_t last = lane_get(best, kWave - 1);
+              if (lane == nout) out = ci > last ? last : ci;
+              ++nout;
+            }
+            best = list_insert(best, ci);
           }
         } else if (nk > 8) {
-          best = list_merge(best, wave_sort64_desc(keep ? c : 0ull));
+          const uint64_t srt = wave_sort64_desc(keep ? c : 0ull);
+          if (SPILL) {
+            const uint64_t rs = lane_reverse(srt);
+            out = best < rs ? best : rs;  // the 64 smallest of list and batch
+          }
+          best = list_merge(best, srt);
+        }
+        if (SPILL) {
+          const float edge = composite_z(lane_get(best, 0)) + ln_lo;
+          spill(out, edge);
+          spill(keep ? 0ull : c, edge);
         }
       }
+      // the k-th best is a lower bound of what is kept (band rows: the queue's top bounds
+      // the band's edge, which the streaming waves track themselves)
       const uint64_t kth = lane_get(best, k - 1);
-      if (kth != 0ull || (band && best != 0ull)) {
-        // the k-th best, or (band) the best so far + ln_lo, is a lower bound of what is kept
-        float kz = kth != 0ull ? composite_z(kth) : -FLT_MAX;
-        if (band) kz = fmaxf(kz, composite_z(lane_get(best, 0)) + ln_lo);
+      if (!band && kth != 0ull) {
+        const float kz = composite_z(kth);
         if (kz > pub) {
           pub = kz;
           if (lane == 0) __atomic_store_n(&s.fin_thr, __float_as_uint(kz), __ATOMIC_RELAXED);
@@ -401,14 +458,26 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     // If the k-th best candidate is at or above the highest of them, nothing in the top k
     // was skipped. Otherwise the row is solved exactly.
     const uint32_t tm = s.tmax;
+    bool spilled = false;  // a band row whose band reaches into the spill
     if constexpr (band) {
       // the band's lower edge; a full list whose last entry is still inside it may have
-      // dropped members of the band
+      // dropped members of the band (rows drawn here: those are in the spill, unless it
+      // overflowed)
       const uint64_t top = lane_get(best, 0);
       const float edge = composite_z(top) + ln_lo;
       if (tm != 0u && (top == 0ull || order_key(edge) < tm)) flags |= kFlagOverflow;
-      const uint64_t last = lane_get(best, kWave - 1);
-      if (last != 0ull && composite_z(last) >= edge) flags |= kFlagOverflow;
+      if constexpr (SPILL) {
+        if (nsp > kTkSpill) {
+          flags |= kFlagOverflow;
+        } else {
+          bool in = false;
+          for (int i = lane; i < nsp; i += kWave) in |= composite_z(s.spill[i]) >= edge;
+          spilled = __ballot(in) != 0ull;
+        }
+      } else {
+        const uint64_t last = lane_get(best, kWave - 1);
+        if (last != 0ull && composite_z(last) >= edge) flags |= kFlagOverflow;
+      }
     } else if (tm != 0u) {
       const uint64_t kth = lane_get(best, k - 1);
       if (kth == 0ull || (uint32_t)(kth >> 32) < tm) flags |= kFlagOverflow;
@@ -417,6 +486,17 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     if (exact && lane == 0) {
       s.verdict = 0;
       if constexpr (band) s.band_top = (uint32_t)(lane_get(best, 0) >> 32);  // 0: an empty list
+    }
+    if (SPILL && !(flags & (kFlagOverflow | kFlagBadHistory | kFlagInvalid)) && spilled) {
+      // the whole workgroup draws over the list and the spill after the closing barrier
+      const int nl = list_count(best);
+      if (lane < nl) s.spill[nsp + lane] = best;
+      if (lane == 0) {
+        s.verdict = 2;
+        s.spill_n = nsp + nl;
+        s.band_top = (uint32_t)(lane_get(best, 0) >> 32);
+      }
+      exact = true;  // the list alone is not the answer
     }
   } else {
     // ---- A. the history ids go into the bitmap (and the count table) while the first
@@ -472,7 +552,14 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         if ((L.bitmap[off >> 5] >> (off & 31)) & 1u)
           lm = hist_inline ? penalize(lm, count_of(id), a.pen) : -INFINITY;
       }
-      sample_add(s.hist, order_key(lm + 0.0f));
+      if constexpr (band) {
+        // band rows take the sample's largest, the final z of a real id, as a lower bound
+        // of zmax (and the threshold its band's edge)
+        const uint32_t km = wave_max(order_key(lm + 0.0f));
+        if (lane == 0) atomicMax(&s.qtop, km);
+      } else {
+        sample_add(s.hist, order_key(lm + 0.0f));
+      }
       wave_lds_sync();
     }
     load(ib, bb, true);
@@ -493,12 +580,17 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     // the finisher's k-th best are exact lower bounds
     uint32_t tmax_w = 0u;
     auto refresh = [&]() {
+      if constexpr (band) {
+        // the band's edge below the largest final z sampled or queued so far: every member
+        // of the band passes it
+        const uint32_t qt = __atomic_load_n(&s.qtop, __ATOMIC_RELAXED);
+        const float tn = qt != 0u ? key_value(qt) + ln_lo : -FLT_MAX;
+        if (tn > thr) set_thr(tn);
+        return;
+      }
       const float ts = sample_threshold(s.hist, (uint32_t)k);
-      float tc = fmaxf(sample_threshold(s.chist, (uint32_t)k),
-                       __uint_as_float(__atomic_load_n(&s.fin_thr, __ATOMIC_RELAXED)));
-      // band: the bin edge of the largest final z queued bounds zmax from below (not the
-      // sample's largest, which may be a history id that a penalty lowers)
-      if constexpr (band) tc = fmaxf(tc, sample_threshold(s.chist, 1u) + ln_lo);
+      const float tc = fmaxf(sample_threshold(s.chist, (uint32_t)k),
+                             __uint_as_float(__atomic_load_n(&s.fin_thr, __ATOMIC_RELAXED)));
       if (ts > thr && ts > tc) tmax_w = order_key(ts);
       const float tn = fmaxf(ts, tc);
       if (tn > thr) set_thr(tn);
@@ -516,13 +608,18 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       const uint64_t m = __ballot(tk);
       if (!m) return;
       uint32_t base = 0u;
-      if (lane == 0) base = atomicAdd(&s.q_tail, (uint32_t)__popcll(m));
+      uint32_t km = 0u;
+      if constexpr (band) km = wave_max(tk ? order_key(v + 0.0f) : 0u);
+      if (lane == 0) {
+        base = atomicAdd(&s.q_tail, (uint32_t)__popcll(m));
+        if (band) atomicMax(&s.qtop, km);
+      }
       base = lane_get(base, 0);
       if (tk) {
         const uint32_t p = base + (uint32_t)lanes_below(m);
         // the ring slot is free once the finisher has taken the entry kTkQueue places back
         const uint64_t c = composite(v + 0.0f, id);
-        sample_add(s.chist, (uint32_t)(c >> 32));
+        if (!band) sample_add(s.chist, (uint32_t)(c >> 32));
         while (p - __atomic_load_n(&s.q_head, __ATOMIC_RELAXED) >= (uint32_t)kTkQueue) __builtin_amdgcn_s_sleep(1);
         __atomic_store_n(&s.queue[p & (kTkQueue - 1)], c, __ATOMIC_RELAXED);
       }
@@ -632,7 +729,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         const float zl = lm * a.inv_t + 0.0f;
         const uint32_t key = lm > -INFINITY && !is_invalid(zl) ? order_key(zl) : 0u;
         float tb = -FLT_MAX;
-        if (__popcll(__ballot(key != 0u)) >= k) tb = key_value(wave_kth_key(key, k));
+        if (!band && __popcll(__ballot(key != 0u)) >= k) tb = key_value(wave_kth_key(key, k));
         if constexpr (band) {
           const uint32_t km = wave_max(key);
           if (km != 0u) tb = fmaxf(tb, key_value(km) + ln_lo);
@@ -736,7 +833,11 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     }
   }
   __syncthreads();
-  if (s.verdict == 0) {
+  if (SPILL && s.verdict == 2) {
+    // every member of the band is in the list or the spill
+    draw_band_candidates<kTkBlock>(a, row, s.spill, s.spill_n, s.band_top, u_row,
+                                   reinterpret_cast<unsigned char*>(L.stage));
+  } else if (s.verdict == 0) {
     if (INLINE && BAND) {
       // a band the list could not hold: one more pass over the row, which is still in the
       // caches, from the list's top (the row's maximum unless candidates were lost)

@@ -88,31 +88,41 @@ def test_large_shape_paths(case):
     assert np.all(ids >= 0)
 
 
-def _flat_top(inp: syn.Inputs, rows, dtype: str, width: int, seed: int) -> syn.Inputs:
-    """The given rows get a plateau: `width` random ids lifted to 4 above the row's maximum
-    (within +-0.05 of each other), so min-p's band holds far more ids than the streaming
-    kernel's 64-entry list and the row goes to the band solver."""
+def _flat_top(inp: syn.Inputs, rows, dtype: str, width, seed: int) -> syn.Inputs:
+    """The given rows get a plateau: `width` random ids (an int, or a list cycled over the
+    rows) lifted to 4 above the row's maximum (within +-0.05 of each other), so min-p's
+    band holds far more ids than the streaming kernel's 64-entry list: up to 1024 of them
+    are drawn from the list and the entries it spilled, more go to the band solver."""
     rng = np.random.default_rng(seed)
+    widths = width if isinstance(width, (list, tuple)) else [width]
     x = inp.logits.copy()
-    for r in rows:
+    for i, r in enumerate(rows):
+        wr = widths[i % len(widths)]
         if dtype == "bf16":
             row = (x[r].astype(np.uint32) << 16).view(np.float32)
         else:
             row = x[r].copy()
         top = float(np.max(row[np.isfinite(row)]))
-        ids = rng.choice(row.size, size=width, replace=False)
-        row[ids] = top + 4.0 + rng.uniform(-0.05, 0.05, size=width).astype(np.float32)
+        ids = rng.choice(row.size, size=wr, replace=False)
+        row[ids] = top + 4.0 + rng.uniform(-0.05, 0.05, size=wr).astype(np.float32)
         x[r] = (row.view(np.uint32) >> 16).astype(np.uint16) if dtype == "bf16" else row
     return syn.Inputs(x, inp.history, inp.mask, inp.uniforms)
 
 
 BAND_CASES = [
-    # (label, batch, vocab, dtype, plateau width, mask) on c4's parameters (min-p 0.05 alone,
-    # frequency and presence penalties, 2048 history ids)
-    ("c4 shape, every other row flat, B=512", 512, 152064, "bf16", 400, False),
-    ("split rows (finished by the finishing kernel), B=4", 4, 152064, "bf16", 2000, False),
-    ("split rows, fp32, masked, B=3", 3, 50000, "f32", 300, True),
-    ("one row, B=1", 1, 32000, "f32", 100, False),
+    # (label, batch, vocab, dtype, plateau width(s), mask, other parameters) on c4's
+    # parameters (min-p 0.05 alone, frequency and presence penalties, history of up to 2048
+    # ids). Rows of a batch of 256 or more are finished by their streaming workgroup: bands
+    # of up to 1024 ids from the list and its spill, wider ones by the band solver.
+    ("c4 shape, every other row flat, B=512", 512, 152064, "bf16", 400, False, {}),
+    ("spill and spill overflow, fp32, B=256", 256, 50000, "f32", [100, 900, 1500, 65], False, {}),
+    ("spill, masked bf16, B=256", 256, 65536, "bf16", [300, 2000, 700], True, {}),
+    ("spill, repetition penalty below 1, B=256", 256, 40000, "f32", [500, 1200], False,
+     {"repetition_penalty": 0.9, "frequency_penalty": 0.0, "presence_penalty": -0.2}),
+    ("spill, whole rows of a small vocabulary, B=8", 8, 8000, "f32", [500, 64, 1000, 3000], False, {}),
+    ("split rows (finished by the finishing kernel), B=4", 4, 152064, "bf16", 2000, False, {}),
+    ("split rows, fp32, masked, B=3", 3, 50000, "f32", 300, True, {}),
+    ("one row, B=1", 1, 32000, "f32", 100, False, {}),
 ]
 
 
@@ -120,9 +130,9 @@ BAND_CASES = [
 def test_band_overflow(case):
     # flat-topped min-p rows go to the band solver, mixed with rows the 64-entry list
     # finishes; both kinds must match the oracle
-    label, B, V, dtype, width, masked = BAND_CASES[case]
+    label, B, V, dtype, width, masked, extra = BAND_CASES[case]
     w = syn.CONFIGS["c4"].scaled(batch=B, vocab=V, dtype=dtype, seed=90 + case,
-                                 hist_len=min(2048, V // 8))
+                                 hist_len=min(2048, V // 8), **extra)
     if masked:
         w = w.scaled(mask_block_frac=0.5, mask_scatter=8)
     print(f"[band {case}] {label}: B={B} V={V} {dtype} plateau {width}", flush=True)
