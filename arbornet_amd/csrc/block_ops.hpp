@@ -46,7 +46,7 @@ __device__ T block_reduce_min(T v, T* scratch) {
 
 // Exclusive prefix sum across the block in thread order; *total gets the block sum.
 template <int BLOCK, typename T>
-__device__ T block_scan_excl(T v, T* scratch, T* total) {
+__device__ __forceinline__ T block_scan_excl(T v, T* scratch, T* total) {
   const T incl = wave_scan_incl(v);
   const int w = threadIdx.x / kWave;
   __syncthreads();

@@ -608,7 +608,8 @@ static int sample_impl(const arbor_sampling_params* p, const void* logits, const
   pl.mask_lds = -1;
   if (allow_mask && pl.path == Path::Stream && p->dtype == ARBOR_DTYPE_F32) {
     pl.mask_lds = (int)pl.lds_stream;
-    pl.lds_stream += sizeof(uint32_t) * (size_t)(pl.chunk_len / 32);
+    // the mask words, then the list of the units that hold an allowed id
+    pl.lds_stream += sizeof(uint32_t) * (size_t)(pl.chunk_len / 32) + sizeof(uint16_t) * arbor::kTkUnitList;
   }
   if (!workspace || workspace_bytes < pl.total)
     return fail(ARBOR_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? workspace_bytes : 0,

@@ -68,6 +68,7 @@ constexpr int kTkQueue = 1024;              // candidate ring between the stream
 constexpr int kSampleBits = 12;             // threshold histogram: top 12 bits of the order key
 constexpr int kSampleBins = 1 << kSampleBits;
 constexpr int kTkSpill = 960;               // min-p band entries the finisher may spill (+ 64 in its list)
+constexpr int kTkUnitList = 8192;           // masked fp32 rows: listed units with an allowed id (16-bit)
 constexpr int kBufferWord3 = 0x00020000;    // buffer resource word 3 (gfx9 family: 32-bit data format)
 constexpr int kBufferNt = 2;                // buffer load cache policy: non-temporal
 static_assert((kTkQueue & (kTkQueue - 1)) == 0, "the ring size is a power of two");
@@ -211,7 +212,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   const void* xrow = row_ptr<DT>(a, row);
   const uint32_t* mrow = MASK ? a.mask + (size_t)row * (size_t)a.mask_words : nullptr;
   const int n_units = (c1 - c0 + VEC - 1) / VEC;
-  const int n_batches = (n_units + kBatch - 1) / kBatch;
+  int n_batches = (n_units + kBatch - 1) / kBatch;  // masked fp32 rows with a unit list: fewer
   // BAND: min-p as the only filter (top_k 0); the list is the whole 64 entries, and it
   // must hold every id of the band z >= zmax + ln(min_p); ln_lo is that bound's
   // safety-margined log
@@ -224,6 +225,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   struct Batch {
     uint32_t w[U][4];  // raw 16-byte units
     uint32_t mw[U];    // mask word of each unit
+    int un[U];         // masked fp32 rows: the chunk's unit number of each slot
   };
   // Aligned rows are read with range-checked buffer loads over the chunk: every lane
   // issues one 16-byte load per unit, and a unit past the chunk reads as zeros without a
@@ -242,13 +244,25 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   // rows load each unit's word beside its logits (measured faster for them).
   constexpr bool SKIP = MASK && DT == ARBOR_DTYPE_F32;
   const uint32_t* lmask = SKIP ? reinterpret_cast<const uint32_t*>(smem + a.mask_lds) : nullptr;
+  // Their batches after the first ones visit only the units that hold an allowed id: the
+  // first batches read the chunk's first kTkStream * kBatch units in order, and later ones
+  // take the rest from a list of those units (LDS, after the mask words), built while the
+  // first batch is in flight; a chunk with more of them than the list holds walks every
+  // unit (n_list < 0).
+  const uint16_t* ulist = SKIP ? reinterpret_cast<const uint16_t*>(smem + a.mask_lds + 4 * (a.chunk_len / 32)) : nullptr;
+  int n_list = -1;
   constexpr uint32_t kUnitBits = (1u << VEC) - 1u;
   constexpr int kPastChunk = 0x7FFFFFF0;  // a buffer offset past every chunk: reads zeros, no access
   // from_lds: the mask words are in LDS (every batch after the first)
   auto load = [&](int bi, Batch& bt, bool from_lds) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int unit = bi * kBatch + u * kWave + lane;
+      int unit = bi * kBatch + u * kWave + lane;
+      if (SKIP && from_lds && n_list >= 0 && bi >= kTkStream) {
+        const int li = unit - kTkStream * kBatch;
+        unit = li < n_list ? (int)ulist[li] : n_units;
+      }
+      if (SKIP) bt.un[u] = unit;
       uint32_t mw = 0u;
       bool skip = false;
       if (SKIP && from_lds) {
@@ -275,19 +289,25 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       if (MASK) bt.mw[u] = mw;
     }
   };
-  auto unit_of = [&](int b, int q) { return b * kBatch + (q / VEC) * kWave + lane; };
-  auto id_of = [&](int b, int q) { return c0 + unit_of(b, q) * VEC + (q % VEC); };
+  auto unit_of = [&](int b, const Batch& bt, int q) -> int {
+    if constexpr (SKIP) return bt.un[q / VEC];
+    return b * kBatch + (q / VEC) * kWave + lane;
+  };
+  auto id_of = [&](int b, const Batch& bt, int q) { return c0 + unit_of(b, bt, q) * VEC + (q % VEC); };
   // element q of a batch is past the chunk or masked (mw: its unit's mask word)
-  auto dropped_w = [&](int b, int q, uint32_t mw) -> bool {
-    const int unit = unit_of(b, q);
+  // (dropped_u: the same for a slot of unit `unit`)
+  auto dropped_u = [&](int unit, int q, uint32_t mw) -> bool {
     if (unit >= n_units) return true;
     if (!ALIGNED && c0 + unit * VEC + (q % VEC) >= c1) return true;
     return MASK && !((mw >> (((c0 + unit * VEC) & 31) + (q % VEC))) & 1u);
   };
+  auto dropped_w = [&](int b, const Batch& bt, int q, uint32_t mw) -> bool {
+    return dropped_u(unit_of(b, bt, q), q, mw);
+  };
   // tempered logit of slot q for the threshold sample: ids past the chunk, masked ids and
   // NaN / +inf read as -inf
   auto zsample = [&](int b, const Batch& bt, int q) __attribute__((always_inline)) -> float {
-    if (dropped_w(b, q, MASK ? bt.mw[q / VEC] : 0u)) return -INFINITY;
+    if (dropped_w(b, bt, q, MASK ? bt.mw[q / VEC] : 0u)) return -INFINITY;
     const float v = unpack_unit<DT>(bt.w[q / VEC], q % VEC) * a.inv_t;
     return is_invalid(v) ? -INFINITY : v;
   };
@@ -352,6 +372,46 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       for (int i = t; i < (1 << a.hash_bits); i += kTkBlock) L.htab[i] = kEmptySlot;
   }
   __syncthreads();
+  if constexpr (SKIP) {
+    constexpr int U0 = kTkStream * kBatch;  // units of the first batches
+    static_assert(U0 * VEC % 32 == 0, "the first batches end on a mask word");
+    if (n_units > U0) {
+      // bit j: unit 8 w + j (VEC = 4 ids per unit) is in the chunk and holds an allowed id
+      auto unit_bits = [&](int w) -> uint32_t {
+        uint32_t nz = lmask[w];
+        nz |= nz >> 1;
+        nz |= nz >> 2;
+        uint32_t bits = 0u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bits |= ((nz >> (4 * j)) & 1u) << j;
+        const int in_chunk = n_units - 8 * w;
+        return in_chunk >= 8 ? bits : bits & ((1u << in_chunk) - 1u);
+      };
+      // each thread lists the units of a run of mask words, at its place in the block's scan
+      const int w0 = U0 * VEC / 32, w1 = (n_units * VEC + 31) / 32;
+      const int per = (w1 - w0 + kTkBlock - 1) / kTkBlock;
+      const int wa = w0 + t * per, wb = min(w1, wa + per);
+      int cnt = 0;
+      for (int w = wa; w < wb; ++w) cnt += __popc(unit_bits(w));
+      __shared__ int s_scan[kTkWaves];
+      int total;
+      const int base = block_scan_excl<kTkBlock, int>(cnt, s_scan, &total);
+      if (total <= kTkUnitList) {
+        uint16_t* ul = const_cast<uint16_t*>(ulist);
+        int p = base;
+        for (int w = wa; w < wb; ++w) {
+          uint32_t bits = unit_bits(w);
+          while (bits) {
+            ul[p++] = (uint16_t)(8 * w + __builtin_ctz(bits));
+            bits &= bits - 1u;
+          }
+        }
+        n_list = total;
+        n_batches = kTkStream + (total + kBatch - 1) / kBatch;
+      }
+      __syncthreads();
+    }
+  }
   if (a.write_probs) {
     float* prow = a.out_probs + (size_t)row * (size_t)a.V;
     for (int i = c0 + t; i < c1; i += kTkBlock) prow[i] = 0.0f;
@@ -536,19 +596,19 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     }
     {
       float lm = -INFINITY;
-      int lq = 0;
+      int lid = 0;  // its id
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         const float v = zsample(ia, ba, q);
         if (v > lm) {
           lm = v;
-          lq = q;
+          lid = id_of(ia, ba, q);
         }
       }
       if (PEN && lm > -INFINITY) {
         // as in the stream: a history id is penalised, or (when a penalty may raise it, and
         // the row's first chunk scores every history id at the end) left out
-        const int id = id_of(ia, lq), off = id - c0;
+        const int id = lid, off = id - c0;
         if ((L.bitmap[off >> 5] >> (off & 31)) & 1u)
           lm = hist_inline ? penalize(lm, count_of(id), a.pen) : -INFINITY;
       }
@@ -638,7 +698,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     auto passes = [&](int b, const Batch& bt, int q) __attribute__((always_inline)) -> bool {
       const float x = unpack_unit<DT>(bt.w[q / VEC], q % VEC);
       bool p = !(x < x_thr);
-      if (MASK) p = p && ((bt.mw[q / VEC] >> (((c0 + unit_of(b, q) * VEC) & 31) + (q % VEC))) & 1u);
+      if (MASK) p = p && ((bt.mw[q / VEC] >> (((c0 + unit_of(b, bt, q) * VEC) & 31) + (q % VEC))) & 1u);
       return p;
     };
     // one candidate per lane whose raw logit passed. When more than k of the wave's lanes
@@ -705,7 +765,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
             if (ns + c <= kTkStage) {
               if (p)
                 stage[ns + lanes_below(m)] =
-                    ((uint64_t)__float_as_uint(unpack_unit<DT>(bt.w[q / VEC], q % VEC)) << 32) | (uint32_t)id_of(b, q);
+                    ((uint64_t)__float_as_uint(unpack_unit<DT>(bt.w[q / VEC], q % VEC)) << 32) | (uint32_t)id_of(b, bt, q);
               ns += c;
             } else {
               full = true;
@@ -724,7 +784,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         float lm = -INFINITY;
 #pragma unroll
         for (int q = 0; q < NQ; ++q)
-          if (passes(b, bt, q) && !dropped_w(b, q, MASK ? bt.mw[q / VEC] : 0u))
+          if (passes(b, bt, q) && !dropped_w(b, bt, q, MASK ? bt.mw[q / VEC] : 0u))
             lm = fmaxf(lm, unpack_unit<DT>(bt.w[q / VEC], q % VEC));
         const float zl = lm * a.inv_t + 0.0f;
         const uint32_t key = lm > -INFINITY && !is_invalid(zl) ? order_key(zl) : 0u;
@@ -752,16 +812,18 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
           float x = 0.0f;
           uint32_t mw = 0u;
           bool p = false;
+          int un = 0;
 #pragma unroll
           for (int qq = 0; qq < NQ; ++qq) {
             if (qq == q) {
               x = unpack_unit<DT>(bt.w[qq / VEC], qq % VEC);
               mw = MASK ? bt.mw[qq / VEC] : 0u;
               p = passes(b, bt, qq);
+              un = unit_of(b, bt, qq);
             }
           }
           if (!__ballot(p)) continue;
-          consider(p && !dropped_w(b, q, mw), x, id_of(b, q));
+          consider(p && !dropped_u(un, q, mw), x, c0 + un * VEC + (q % VEC));
         }
       }
     };

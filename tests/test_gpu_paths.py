@@ -46,6 +46,17 @@ CASES = [
     ("c4 inputs, top-p 0.9 + min-p 0.05, B=64", -64, 152064, "bf16", dict(top_p=0.9), 4),
     ("c4 inputs, top-p 0.9 + min-p 0.05, B=256", -256, 152064, "bf16", dict(top_p=0.9), 4),
     ("c4 inputs, top-p 0.3 + min-p 0.01, B=64", -64, 152064, "bf16", dict(top_p=0.3, min_p=0.01), 4),
+    # masked fp32 rows streamed whole: after their first batches they visit only the units
+    # that hold an allowed id, from an LDS list of up to 8192 units; denser masks walk every
+    # unit
+    ("masked stream, sparse mask (unit list), B=256", 256, 128256, "f32",
+     dict(top_k=20, top_p=0.9, repetition_penalty=1.0, hist_len=0, mask_block_frac=0.02, mask_scatter=300), 2),
+    ("masked stream, dense mask (list overflows), B=256", 256, 152064, "f32",
+     dict(top_k=50, top_p=0.95, mask_block_frac=0.9, mask_scatter=64), 2),
+    ("masked stream, min-p band, sparse mask, B=256", 256, 100000, "f32",
+     dict(top_p=1.0, min_p=0.05, mask_block_frac=0.05, mask_scatter=32), 2),
+    ("masked split rows, sparse mask, B=8", 8, 128256, "f32",
+     dict(top_k=20, top_p=0.9, mask_block_frac=0.05, mask_scatter=32), 2),
 ]
 
 
