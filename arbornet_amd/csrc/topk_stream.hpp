@@ -470,7 +470,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         const uint64_t km = __ballot(keep);
         const int nk = __popcll(km);
         uint64_t out = 0ull;
-        if (nk > 0 && nk <= 8) {
+        if (nk > 0 && nk <= 16) {
           uint64_t rest = km;
           int nout = 0;
           while (rest) {
@@ -486,7 +486,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
             }
             best = list_insert(best, ci);
           }
-        } else if (nk > 8) {
+        } else if (nk > 16) {
           const uint64_t srt = wave_sort64_desc(keep ? c : 0ull);
           if (SPILL) {
             const uint64_t rs = lane_reverse(srt);
