@@ -498,13 +498,14 @@ __global__ void __launch_bounds__(kNuBlock) nucleus_kernel(Args a, NuRec* recs, 
     }
     for (int g = t; g < kNuGroups; g += kNuBlock) pub_store(&mine->gsum[g], gsum[g]);
     sync_row();  // B1
+    // lane c reads chunk c's record (S <= 64): one round trip instead of S
     uint32_t km = 0u, fl = 0u;
-    for (int c = 0; c < S; ++c) {
-      km = max(km, pub_load(&rowr[c].kmax));
-      fl |= pub_load(&rowr[c].flags);
+    if (lane < S) {
+      km = pub_load(&rowr[lane].kmax);
+      fl = pub_load(&rowr[lane].flags);
     }
-    kmax = km;
-    flags = fl;
+    kmax = wave_max(km);
+    flags = wave_reduce(fl, [](uint32_t x, uint32_t y) { return x | y; });
   } else {
     kmax = s.kmax;
     flags = s.flags;
@@ -538,9 +539,20 @@ __global__ void __launch_bounds__(kNuBlock) nucleus_kernel(Args a, NuRec* recs, 
       double gm0 = 0.0, gm1 = 0.0;
       const int g0 = kNuGroups - 1 - 2 * lane, g1 = g0 - 1;
       if (S > 1) {
-        for (int c = 0; c < S; ++c) {
-          gm0 += pub_load(&rowr[c].gsum[g0]);
-          gm1 += pub_load(&rowr[c].gsum[g1]);
+        for (int cb = 0; cb < S; cb += 4) {
+          double x0[4], x1[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            x0[j] = cb + j < S ? pub_load(&rowr[cb + j].gsum[g0]) : 0.0;
+            x1[j] = cb + j < S ? pub_load(&rowr[cb + j].gsum[g1]) : 0.0;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (cb + j < S) {
+              gm0 += x0[j];
+              gm1 += x1[j];
+            }
+          }
         }
       } else {
         gm0 = gsum[g0];
@@ -582,7 +594,13 @@ __global__ void __launch_bounds__(kNuBlock) nucleus_kernel(Args a, NuRec* recs, 
       const int bin = gsel * kWave + kWave - 1 - lane;
       uint64_t wsum = 0ull;
       if (S > 1) {
-        for (int c = 0; c < S; ++c) wsum += pub_load(&rowr[c].gbins[kWave - 1 - lane]);
+        for (int cb = 0; cb < S; cb += 4) {
+          uint64_t x[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[j] = cb + j < S ? pub_load(&rowr[cb + j].gbins[kWave - 1 - lane]) : 0ull;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) wsum += x[j];
+        }
       } else {
         wsum = hist[bin];
       }
@@ -725,24 +743,58 @@ __global__ void __launch_bounds__(kNuBlock) nucleus_kernel(Args a, NuRec* recs, 
     last_row = -1;
     flags_c = 0u;
     n = 0;
-    for (int c = 0; c < S; ++c) {
-      Erow += pub_load(&rowr[c].E);
-      above += pub_load(&rowr[c].above);
-      last_row = max(last_row, pub_load(&rowr[c].last));
-      flags_c |= pub_load(&rowr[c].flags);
-      const int nc = pub_load(&rowr[c].ncoll);
-      if (t == 0) s.coff[c] = n;
-      if (nc > kNuCollChunk || n + nc > kNuColl) flags_c |= kNuFlagFallback;
-      n = min(n + min(nc, kNuCollChunk), kNuColl);
+    for (int cb = 0; cb < S; cb += 4) {
+      // the records of up to 4 chunks in flight, combined in chunk order
+      double xe[4], xa[4];
+      int32_t xl[4], xn[4];
+      uint32_t xf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool in = cb + j < S;
+        xe[j] = in ? pub_load(&rowr[cb + j].E) : 0.0;
+        xa[j] = in ? pub_load(&rowr[cb + j].above) : 0.0;
+        xl[j] = in ? pub_load(&rowr[cb + j].last) : -1;
+        xf[j] = in ? pub_load(&rowr[cb + j].flags) : 0u;
+        xn[j] = in ? pub_load(&rowr[cb + j].ncoll) : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (cb + j >= S) break;
+        Erow += xe[j];
+        above += xa[j];
+        last_row = max(last_row, xl[j]);
+        flags_c |= xf[j];
+        const int nc = xn[j];
+        if (t == 0) s.coff[cb + j] = n;
+        if (nc > kNuCollChunk || n + nc > kNuColl) flags_c |= kNuFlagFallback;
+        n = min(n + min(nc, kNuCollChunk), kNuColl);
+      }
     }
     if (!(flags_c & kNuFlagFallback)) {
       // every entry at once: entry i of the row belongs to the chunk whose range holds it
       __syncthreads();
-      for (int i = t; i < n; i += kNuBlock) {
-        int c = 0;
-        while (c + 1 < S && s.coff[c + 1] <= i) ++c;
-        gkey[i] = pub_load(&rowr[c].ckey[i - s.coff[c]]);
-        gm[i] = pub_load(&rowr[c].cm[i - s.coff[c]]);
+      static_assert(kNuColl == 4 * kNuBlock, "four collected entries per thread");
+      uint64_t xk[4];
+      float xm[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = t + j * kNuBlock;
+        xk[j] = 0ull;
+        xm[j] = 0.0f;
+        if (i < n) {
+          int c = 0;
+          while (c + 1 < S && s.coff[c + 1] <= i) ++c;
+          xk[j] = pub_load(&rowr[c].ckey[i - s.coff[c]]);
+          xm[j] = pub_load(&rowr[c].cm[i - s.coff[c]]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = t + j * kNuBlock;
+        if (i < n) {
+          gkey[i] = xk[j];
+          gm[i] = xm[j];
+        }
       }
     }
     if (t == 0) s.coff[S] = n;
@@ -842,6 +894,13 @@ __global__ void __launch_bounds__(kNuBlock) nucleus_kernel(Args a, NuRec* recs, 
     if (wave == 0) {
       double acc_before = 0.0, acc_all = 0.0, acc_mine = 0.0;
       int32_t lk = -1, lkm = -1;
+      // lane c holds chunk c's mass above the collected bins and largest kept id (S <= 64)
+      double abv = 0.0;
+      int32_t lst = -1;
+      if (S > 1 && lane < S) {
+        abv = pub_load(&rowr[lane].above);
+        lst = pub_load(&rowr[lane].last);
+      }
       for (int c = 0; c < S; ++c) {
         double cm = 0.0;
         int32_t lc = -1;
@@ -854,11 +913,11 @@ __global__ void __launch_bounds__(kNuBlock) nucleus_kernel(Args a, NuRec* recs, 
           cm += wave_sum(v);
         }
         lc = wave_max(lc);
-        const double ck = (S > 1 ? pub_load(&rowr[c].above) : above_c) + cm;
+        const double ck = (S > 1 ? lane_get(abv, c) : above_c) + cm;
         if (c < chunk) acc_before += ck;
         if (c == chunk) {
           acc_mine = ck;
-          lkm = max(lc, S > 1 ? pub_load(&rowr[c].last) : last_c);
+          lkm = max(lc, S > 1 ? lane_get(lst, c) : last_c);
         }
         acc_all += ck;
         lk = max(lk, lc);
