@@ -118,9 +118,18 @@ __device__ __forceinline__ float sample_threshold(const SampleHist& h, uint32_t 
 // The k-th largest of the lanes' order keys (0 = none), given at least k nonzero keys:
 // the largest prefix with at least k keys at or above it, found bit by bit with ballots.
 __device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, int k) {
-  uint32_t pre = 0u;
-#pragma unroll 4
-  for (int bit = 31; bit >= 0; --bit) {
+  // the bits above the highest one where the nonzero keys differ are common to all of
+  // them; below it, 16 bits are decided (stopping early leaves a smaller prefix that at
+  // least k keys still reach: a lower bound of the k-th largest, which is what the
+  // thresholds need)
+  const uint32_t hi = wave_max(key);
+  const uint32_t lo = wave_min(key != 0u ? key : 0xFFFFFFFFu);
+  const uint32_t diff = hi ^ (lo <= hi ? lo : hi);
+  if (diff == 0u) return hi;  // every nonzero key is the same (k of them are given)
+  const int top = 31 - __builtin_clz(diff);
+  uint32_t pre = top == 31 ? 0u : hi & ~((2u << top) - 1u);
+  const int stop = top >= 16 ? top - 16 : -1;
+  for (int bit = top; bit > stop; --bit) {
     const uint32_t cnd = pre | (1u << bit);
     if (__popcll(__ballot(key >= cnd)) >= k) pre = cnd;
   }
