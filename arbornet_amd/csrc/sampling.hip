@@ -381,6 +381,11 @@ int launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, const ar
 template <int DT, bool PEN, bool MASK, bool ALIGNED, bool BAND>
 int launch_topk5(const Plan& pl, hipStream_t st, const arbor::Args& a) {
   const dim3 grid((unsigned)(a.B * pl.S)), block(arbor::kTkBlock);
+  if constexpr (ALIGNED && !MASK) {
+    // rows the plan finishes in one workgroup and that fit one round of requests
+    if (pl.S == 1 && a.V <= arbor::tk_whole_max_ids(arbor::Elem<DT>::kVec))
+      return launch(arbor::topk_kernel<DT, PEN, false, true, true, BAND, true>, grid, block, pl.lds_stream, st, a);
+  }
   int r = pl.inline_fin
               ? launch(arbor::topk_kernel<DT, PEN, MASK, true, ALIGNED, BAND>, grid, block, pl.lds_stream, st, a)
               : launch(arbor::topk_kernel<DT, PEN, MASK, false, ALIGNED, BAND>, grid, block, pl.lds_stream, st, a);
@@ -614,6 +619,22 @@ static int sample_impl(const arbor_sampling_params* p, const void* logits, const
   if (!workspace || workspace_bytes < pl.total)
     return fail(ARBOR_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace ? workspace_bytes : 0,
                 pl.total);
+  // short unmasked rows of whole aligned 16-byte units: one workgroup per row requests the
+  // whole row at once (topk_kernel's WHOLE instances; the workspace the plan asked for
+  // covers this, which needs none)
+  {
+    const size_t esz_ = p->dtype == ARBOR_DTYPE_BF16 ? 2 : 4;
+    const int vec = p->dtype == ARBOR_DTYPE_BF16 ? 8 : 4;
+    const bool aligned_ = ((uintptr_t)logits % 16 == 0) && (((size_t)p->ld_logits * esz_) % 16 == 0);
+    if (pl.path == Path::Stream && !allow_mask && aligned_ && p->vocab % vec == 0 &&
+        p->vocab <= arbor::tk_whole_max_ids(vec)) {
+      pl.S = 1;
+      pl.chunk_len = (int)align_up((size_t)p->vocab, 512);
+      pl.inline_fin = true;
+      pl.bitmap_words = p->hist_len > 0 ? pl.chunk_len / 32 : 0;
+      pl.lds_stream = arbor::TkLds::bytes(pl.bitmap_words, p->hist_len > 0 ? (1 << pl.hash_bits) : 0);
+    }
+  }
 
   arbor::Args a{};
   a.logits = logits;

@@ -80,6 +80,12 @@ static_assert((kTkQueue & (kTkQueue - 1)) == 0, "the ring size is a power of two
 #ifndef TK_UNITS_F32
 #define TK_UNITS_F32 2
 #endif
+// Short unmasked aligned rows (WHOLE): one workgroup per row, every wave requests all
+// three batches of its ring (three 16-byte units per lane each) at the start, so the row's
+// selection waits for one memory latency instead of one per round of the ring; rows of up
+// to kTkStream * 64 * 9 units (34,560 fp32 or 69,120 bf16 ids).
+constexpr int kTkWholeUnits = 3;
+__host__ __device__ constexpr int tk_whole_max_ids(int vec) { return kTkStream * kWave * 3 * kTkWholeUnits * vec; }
 template <int DT, bool MASK, bool ALIGNED>
 struct TkUnits {
   static constexpr int value = DT == ARBOR_DTYPE_F32 ? TK_UNITS_F32 : (MASK || !ALIGNED ? 2 : 3);
@@ -181,8 +187,9 @@ static_assert(kTkSpill + kWave <= kTkBlock, "a band draw takes one candidate per
 static_assert(band_lds_bytes(kMaxChunkLen, kTkBlock) <= sizeof(uint64_t) * kTkStream * kTkStage,
               "the band solver's scratch of a whole-row chunk fits the stages");
 
-template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED, bool BAND>
+template <int DT, bool PEN, bool MASK, bool INLINE, bool ALIGNED, bool BAND, bool WHOLE = false>
 __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
+  static_assert(!WHOLE || (INLINE && ALIGNED && !MASK), "whole rows: unmasked, aligned, finished here");
   // Every kernel argument the stream uses is read at entry: a scalar load of the argument
   // segment issued later would be one more memory round trip while the first batches are
   // in flight (the compiler otherwise loads them where they are first used).
@@ -191,7 +198,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
                    "s"(a.hash_bits), "s"(a.bitmap_words), "s"(a.mask_lds), "s"(a.write_probs), "s"(a.pen_mono), "s"(a.top_p),
                    "s"(a.min_p), "s"(a.out_ids), "s"(a.out_probs));
   constexpr int VEC = Elem<DT>::kVec;
-  constexpr int U = TkUnits<DT, MASK, ALIGNED>::value;
+  constexpr int U = WHOLE ? kTkWholeUnits : TkUnits<DT, MASK, ALIGNED>::value;
   constexpr int NQ = VEC * U;        // elements per lane per batch
   constexpr int kBatch = U * kWave;  // units per batch
   constexpr int HIDR = ARBOR_HISTORY_MAX / (kTkStream * kWave) + 1;  // history ids per streaming lane
@@ -355,6 +362,10 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
   Batch ba, bb, bc;
   int ia = finisher ? n_batches : wave, ib = wave + kTkStream, ic = wave + 2 * kTkStream;
   load(ia, ba, false);
+  if constexpr (WHOLE) {  // the rest of the wave's share (past the chunk: zeros, no access)
+    load(ib, bb, false);
+    load(ic, bc, false);
+  }
   if (SKIP) {
     uint32_t* lm = reinterpret_cast<uint32_t*>(smem + a.mask_lds);
     for (int i = t; i < (c1 - c0 + 31) / 32; i += kTkBlock) lm[i] = mrow[(c0 >> 5) + i];
@@ -631,8 +642,10 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       }
       wave_lds_sync();
     }
-    load(ib, bb, true);
-    load(ic, bc, true);
+    if constexpr (!WHOLE) {
+      load(ib, bb, true);
+      load(ic, bc, true);
+    }
 
     // ---- B. stream ----
     uint64_t* stage = L.stage + wave * kTkStage;
@@ -673,7 +686,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       return b;
     };
     // queue the lanes' candidates (final z) for the finisher
-    auto emit = [&](bool tk, float v, int id) {
+    auto emit = [&](bool tk, float v, int id) __attribute__((always_inline)) {
       const uint64_t m = __ballot(tk);
       if (!m) return;
       uint32_t base = 0u;
@@ -714,7 +727,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
     // hold one at or above the threshold, the k-th largest of them (final z) is a lower
     // bound of the row's k-th best and becomes the wave's threshold (this bounds what is
     // queued while the threshold is still far below the row's k-th best).
-    auto consider = [&](bool tk, float x, int id) {
+    auto consider = [&](bool tk, float x, int id) __attribute__((always_inline)) {
       float v = -INFINITY;
       if (tk) {
         v = x * a.inv_t;
@@ -739,7 +752,7 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
       emit(tk, v, id);
     };
     // Staged raw candidates (x bits << 32 | id), 64 per round across the lanes.
-    auto absorb = [&](int ns) {
+    auto absorb = [&](int ns) __attribute__((always_inline)) {
 #pragma unroll 1
       for (int j = 0; j < ns; j += kWave) {
         const int i = j + lane;
@@ -836,7 +849,16 @@ __global__ void __launch_bounds__(kTkBlock) topk_kernel(Args a) {
         }
       }
     };
-    for (;;) {
+    if constexpr (WHOLE) {
+      // the wave's three batches are its whole share of the row
+      if (ia < n_batches) {
+        refresh();
+        process(ia, ba);
+      }
+      if (ib < n_batches) process(ib, bb);
+      if (ic < n_batches) process(ic, bc);
+    }
+    for (; !WHOLE;) {
       if (ia >= n_batches) break;
       refresh();
       process(ia, ba);
